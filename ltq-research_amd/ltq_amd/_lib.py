@@ -1,0 +1,58 @@
+"""Loader of the gfx950 HIP library (libltq_hip.so, built in-tree by ltq-research_amd/build.py).
+
+There is no fallback: if the library or the device is missing, every entry point raises. The C ABI is
+declared in include/ltq_hip.h; argument conventions follow the reference's ctypes glue
+(src/tcq_proto.py:515-534)."""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+_SO = Path(__file__).resolve().parent / "libltq_hip.so"
+_LIB = None
+
+vp, ci, cf, cl = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_long
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    # src/cuda/tcq_viterbi.cu:743-746; ctypes argtypes as src/tcq_proto.py:529
+    "tcq_viterbi": (ci, [vp] * 15 + [ci] * 18 + [vp, ci, vp]),
+    # src/cuda/tcq_viterbi.cu:806-807; src/tcq_proto.py:531-532
+    "lut_subs_quant": (ci, [vp] * 4 + [ci, cf, cf, ci, vp]),
+}
+
+
+class LtqLibraryMissing(RuntimeError):
+    pass
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        if not _SO.exists():
+            raise LtqLibraryMissing(f"{_SO} is not built: run `python -c 'import __graft_entry__ as g; g.build()'`")
+        L = ctypes.CDLL(str(_SO))
+        for name, (res, args) in SIGNATURES.items():
+            if hasattr(L, name):
+                fn = getattr(L, name)
+                fn.restype = res
+                fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def require_device(t) -> None:
+    import torch
+    if not torch.cuda.is_available():
+        raise LtqLibraryMissing("no HIP device: the LTQ kernels run only on an MI355X (gfx950)")
+    if not t.is_cuda:
+        raise ValueError("LTQ kernels take device tensors")
+
+
+def stream_ptr():
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ptr(t):
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,114 @@
+"""TCQ format definitions: TCQ_CONFIG, the .ltq tile format description and the format menus.
+
+Mirrors src/liqk_v2.py:779-840 (TCQ_CONFIG construction), src/ltq_format.py:16-66 (NU, TILE, MASK_M,
+LtqFormat, load_formats) and src/equal_bpw.py:42-75 (SETS menus). The trained tables themselves are data,
+extracted unchanged into data/tcq_tables.json (see data/make_tables.py).
+"""
+from __future__ import annotations
+
+import json
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Dict
+
+import numpy as np
+
+QK_K = 256            # weights per tile / per row block (src/iqk_format.py:23)
+SUBBLOCK_SIZE = 16    # weights per gain index (src/iqk_format.py:24)
+NUM_SUBBLOCKS = QK_K // SUBBLOCK_SIZE
+NU = 10               # trellis memory: state = last 10 code bits (src/ltq_format.py:16)
+TILE = 256
+MASK_M = 359          # primary Ungerboeck label mask (src/ltq_format.py:18)
+
+_TABLES = json.loads((Path(__file__).resolve().parent / "data" / "tcq_tables.json").read_text())
+
+
+def _build_config() -> Dict[str, dict]:
+    cfg: Dict[str, dict] = {k: dict(v) for k, v in _TABLES["base"].items()}
+    # R variants: one d per row + 5-bit block exponent, trellis state carried between tiles (liqk_v2.py:826-828)
+    for k, sc in ((2, 1.05), (3, 1.15), (4, 1.25)):
+        cfg[f"TCQ{k}R"] = dict(cfg[f"TCQ{k}"], row_scale=True, carry=True, scale=sc)
+    for name, v in _TABLES["variants"].items():
+        v = dict(v)
+        parent = v.pop("parent")
+        cfg[name] = dict(cfg[parent], **v)
+    # half-integer R formats: alternating K / K+1 tile rows (liqk_v2.py:813-821)
+    for k in (2, 3):
+        cfg[f"TCQ{k}5R"] = {"K": k, "K_hi": k + 1, "nu": 10, "m": 359, "h": 1, "row_scale": True, "carry": True,
+                            "scale": 1.0, "lo": f"TCQ{k}R", "hi": f"TCQ{k + 1}R"}
+    # night-2 tail-biting formats with extended labels (liqk_v2.py:834-840)
+    xs = _TABLES["x_scale"]
+    for name, t in _TABLES["x_tables"].items():
+        cfg[name] = {"K": t["K"], "nu": 10, "m": 359, "h": t["h"], "step": t["step"], "lut": t["lut"],
+                     "sub": t.get("sub", SUBBLOCK_SIZE), "pp": t.get("pp", False), "scale": xs.get(name, 1.0),
+                     "m_extra": tuple(t["m_extra"]), "row_scale": True, "tb": True,
+                     **({"n_cand": 4} if t["h"] > 2 else {})}
+    return cfg
+
+
+TCQ_CONFIG: Dict[str, dict] = _build_config()
+TCQ_X_SCALE: Dict[str, float] = dict(_TABLES["x_scale"])
+
+# format menus (src/equal_bpw.py:47-75)
+_X5 = ["TCQ2X0", "TCQ2X", "TCQ3X1", "TCQ3X", "TCQ4X1", "TCQ4X2", "TCQ4X", "TCQ5X3", "TCQ5X"]
+SETS = {
+    "TCQX": ["TCQ2X0", "TCQ2X", "TCQ3X1", "TCQ3X", "TCQ4X1", "TCQ4X2", "TCQ4X"],
+    "TCQX5": list(_X5),
+    "TCQP": _X5 + ["TCQ4W2", "TCQ4W3", "TCQ25X", "TCQ35X1", "TCQ35X", "TCQ45X"],
+    "TCQPQ": _X5 + ["TCQ4W2", "TCQ4W3", "TCQ25X", "TCQ35X1", "TCQ35X", "TCQ45X", "TCQ275X", "TCQ275X2", "TCQ375X",
+                    "TCQ475X"],
+    "TCQPQE": _X5 + ["TCQ4W2", "TCQ4W3", "TCQ25X", "TCQ35X1", "TCQ35X", "TCQ45X", "TCQ275X", "TCQ275X2", "TCQ375X",
+                     "TCQ475X", "TCQ225X", "TCQ325X", "TCQ425X"],
+}
+
+FRAC_RATE = {0: 0.0, 1: 0.5, 2: 0.25, 3: 0.75}
+
+
+@dataclass(frozen=True)
+class LtqFormat:
+    """One .ltq tile format (src/ltq_format.py:21-54): K bits/weight before the fractional mode, frac (0 none,
+    1 D2, 2 D4), label masks, gain header bits h, gain step, weights per gain index, LUT and the explicit gain
+    table (stored in the file, so that decoders use the quantizer's exact values)."""
+    name: str
+    K: int
+    frac: int
+    masks: tuple
+    h: int
+    step: float
+    sub: int
+    lut: np.ndarray
+    gain_tab: np.ndarray
+
+    @property
+    def n_labels(self) -> int:
+        return 2 ** len(self.masks) * 2
+
+    @property
+    def U(self) -> int:
+        return 1 << (self.K - 1)
+
+    def lsb_words(self, L: int = TILE) -> int:
+        return ({0: L, 1: L // 2, 2: 3 * L // 4}[self.frac] + 15) // 16
+
+    def gain_words(self, L: int = TILE) -> int:
+        return (L // self.sub * self.h + 15) // 16
+
+    def tile_bytes(self, L: int = TILE) -> int:
+        return 2 * (L // 16 + L // 16 * (self.K - 2) + (self.lsb_words(L) if self.K > 1 else 0) + self.gain_words(L))
+
+    def bpw(self, k_in: int) -> float:
+        return self.tile_bytes() * 8 / TILE + 8 / 256 + 16 / k_in
+
+
+def make_format(name: str) -> LtqFormat:
+    from .tcq_proto import make_gains
+    c = TCQ_CONFIG[name]
+    return LtqFormat(name, c["K"], int(c.get("pp", 0)), (c["m"],) + tuple(c.get("m_extra", ())), c["h"],
+                     float(c["step"]), c.get("sub", 16), np.asarray(c["lut"], dtype=np.float32),
+                     make_gains(c["h"], c["step"], "cpu").numpy())
+
+
+def load_formats(menu) -> Dict[str, LtqFormat]:
+    """Formats of a menu (src/ltq_format.py:57-66); gains are evaluated on the CPU (the reference uses the
+    quantizing device, whose pow rounding may differ; the .ltq header stores the table explicitly)."""
+    return {name: make_format(name) for name in menu}

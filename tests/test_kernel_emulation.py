@@ -1,0 +1,60 @@
+"""The gfx950 kernel source (ltq-research_amd/csrc/tcq_kernel.h) compiled for the host and run with one
+thread per lane (tests/emu) must match the oracle bit for bit: pins the register layout, decision-word
+format and traceback indexing on the CPU, for every parity mode, before any GPU run."""
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+sys.path.insert(0, str(Path(__file__).resolve().parent / "emu"))
+
+CASES = [
+    dict(pp=0, ext=(), G=1, T=32),
+    dict(pp=0, ext=(), G=4, T=64),
+    dict(pp=0, ext=(241,), G=2, T=64, init=True, tail=True),
+    dict(pp=0, ext=(), G=2, T=64, S=256),
+    dict(pp=0, ext=(), G=3, T=48, S=256, init=True, tail=True),
+    dict(pp=1, ext=(241,), G=2, T=64),
+    dict(pp=2, ext=(241,), G=4, T=64),
+    dict(pp=2, ext=(241,), G=2, T=64, init=True, tail=True),
+    dict(pp=3, ext=(), G=2, T=64, U=8),
+    dict(pp=2, ext=(241,), G=2, T=64, n_cand=2, Gfull=4),
+    dict(pp=2, ext=(241,), G=4, T=32, ld=64, steps=32, rot=16, mid_t=16),
+    dict(pp=0, ext=(), G=2, T=36, sub=6),
+    dict(pp=0, ext=(40, 475), G=2, T=64, mix=16),
+    dict(pp=2, ext=(211, 397), G=1, T=32),
+]
+
+
+@pytest.mark.parametrize("ci", range(len(CASES)))
+def test_emulated_kernel_matches_oracle(oracle, ci):
+    import emu
+    c = CASES[ci]
+    rng = np.random.default_rng(ci)
+    nl = 4 << len(c["ext"])
+    U = c.get("U", 4)
+    S = c.get("S", 1024)
+    Gf = c.get("Gfull", c["G"])
+    N = 2
+    ld = c.get("ld", c["T"])
+    tab = rng.standard_normal(nl * U).astype(np.float32)
+    gains = (2.0 ** ((np.arange(Gf) - (Gf - 1) / 2) * 0.22)).astype(np.float32)
+    x = (rng.standard_normal((N, ld)) * 1.2).astype(np.float32)
+    w = (rng.random((N, ld)) + 0.5).astype(np.float32)
+    init = rng.integers(0, S, size=N).astype(np.int32) if c.get("init") else None
+    tab_hi = rng.standard_normal(nl * 2 * U).astype(np.float32) if c.get("mix") else None
+    gains_hi = (gains * 1.1).astype(np.float32) if c.get("mix") else None
+    kw = dict(init_st=init, tail=c.get("tail", False), S=S, U=U, sub=c.get("sub", 16), m_extra=c["ext"], pp=c["pp"],
+              n_cand=c.get("n_cand", 0), steps=c.get("steps", 0), rot=c.get("rot", 0), mid_t=c.get("mid_t", 0),
+              tab_hi=tab_hi, gains_hi=gains_hi, mix=c.get("mix", 0))
+    o = oracle.tcq_viterbi(x, w, tab, gains, want_end=True, **kw)
+    e = emu.tcq_viterbi(x, w, tab, gains, **kw)
+    assert np.array_equal(o["best"], e["best"])
+    if kw["mid_t"]:
+        assert np.array_equal(o["mid"], e["mid"])
+    else:
+        assert np.array_equal(o["code"], e["code"])
+        assert np.array_equal(o["rec"].view(np.uint32), e["rec"].view(np.uint32))
+    if o["gcand"] is not None:
+        assert np.array_equal(o["gcand"], e["gcand"])
