@@ -7,61 +7,51 @@
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 
-#include "tcq_kernel.h"
+#include "tcq_launch.h"
 
 namespace ltq {
 
-extern "C" __shared__ __align__(16) char ltq_dyn_smem[];
+// instantiated in tcq_inst_*.hip (compiled in parallel)
+extern template int launch<8, 0, 4>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 0, 4>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 0, 8>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 0, 16>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 0, 32>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 1, 4>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 1, 8>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 1, 16>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 1, 32>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 2, 4>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 2, 8>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 2, 16>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 2, 32>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 3, 4>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 3, 8>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 3, 16>(const TcqArgs&, hipStream_t);
+extern template int launch<10, 3, 32>(const TcqArgs&, hipStream_t);
 
-struct GpuX {
-    __device__ __forceinline__ int tid() const { return (int)threadIdx.x; }
-    __device__ __forceinline__ int tile() const { return (int)blockIdx.x; }
-    __device__ __forceinline__ int nthreads() const { return (int)blockDim.x; }
-    __device__ __forceinline__ void* smem() const { return ltq_dyn_smem; }
-    __device__ __forceinline__ void sync() const { __syncthreads(); }
-    __device__ __forceinline__ void wave_sync() const
-    {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-    // acc = 2 * acc + bit, the bit taken from the compare's lane mask (one v_addc per 64 decisions)
-    __device__ __forceinline__ uint32_t push(uint32_t acc, bool bit) const
-    {
-        const unsigned long long mk = __builtin_amdgcn_ballot_w64(bit);
-        uint32_t out;
-        unsigned long long carry;
-        asm volatile("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(out), "=s"(carry) : "v"(acc), "s"(mk));
-        return out;
-    }
-};
-
-template <int NU, int MD>
-__global__ __launch_bounds__(512) void tcq_viterbi_kernel(TcqArgs a)
+int device_lds_max()
 {
-    GpuX x;
-    tcq_tile<NU, MD>(a, x);
+    static int v = -1;
+    if (v < 0) {
+        int dev = 0, x = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return -1;
+        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) return -1;
+        v = x;
+    }
+    return v;
 }
 
 template <int NU, int MD>
-static int launch(const TcqArgs& a, hipStream_t stream)
+static int launch_nl(const TcqArgs& a, hipStream_t st)
 {
-    const Smem L = smem_layout<NU, MD>(a.T, a.G, a.nl, a.Gfull, a.sub);
-    // decision words of one traceback window must fit in the reused exchange + table region
-    constexpr int WCH = Mode<NU, MD>::FG == 1 ? 4 : 1;
-    if (WCH * a.G * Mode<NU, MD>::NW * 64 * 4 > L.gsel - L.exch) return -1;
-    static int lds_max = -1;
-    if (lds_max < 0) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) != hipSuccess) return -1;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) return -1;
-        (void)hipFuncSetAttribute((const void*)tcq_viterbi_kernel<NU, MD>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, v);
-        lds_max = v;
+    switch (a.nl) {
+        case 4: return launch<NU, MD, 4>(a, st);
+        case 8: return launch<NU, MD, 8>(a, st);
+        case 16: return launch<NU, MD, 16>(a, st);
+        case 32: return launch<NU, MD, 32>(a, st);
+        default: return -1;
     }
-    if (L.total > lds_max) return -1;
-    hipLaunchKernelGGL((tcq_viterbi_kernel<NU, MD>), dim3(a.N), dim3(64 * a.G), L.total, stream, a);
-    return 0;
 }
 
 }  // namespace ltq
@@ -93,11 +83,11 @@ extern "C" int tcq_viterbi(const float* x, const float* w, const float* tab, con
               mid_t, tail, N, T, S, U, G, Gfull, m, sub, U_hi, mix, m2, m3, m4, nl, ld, rot, pbits, pp};
     hipStream_t st = (hipStream_t)stream;
     int rc;
-    if (S == 256) rc = launch<8, 0>(a, st);
-    else if (pp == 0) rc = launch<10, 0>(a, st);
-    else if (pp == 1) rc = launch<10, 1>(a, st);
-    else if (pp == 2) rc = launch<10, 2>(a, st);
-    else rc = launch<10, 3>(a, st);
+    if (S == 256) rc = launch<8, 0, 4>(a, st);
+    else if (pp == 0) rc = launch_nl<10, 0>(a, st);
+    else if (pp == 1) rc = launch_nl<10, 1>(a, st);
+    else if (pp == 2) rc = launch_nl<10, 2>(a, st);
+    else rc = launch_nl<10, 3>(a, st);
     if (rc != 0) return rc;
     return (int)hipGetLastError();
 }

@@ -11,9 +11,11 @@
 
 #include <barrier>
 #include <cstdlib>
+#include <cmath>
 #include <cstring>
 #include <memory>
 #include <thread>
+#include <type_traits>
 #include <vector>
 
 using namespace ltq;
@@ -23,22 +25,47 @@ struct CpuX {
     char* smem_;
     std::barrier<>* blk_;
     std::barrier<>** waves_;
+    uint32_t* xch_;  // per-wave lane exchange for readlane
     int tid() const { return tid_; }
+    int wave() const { return tid_ >> 6; }
     int tile() const { return tile_; }
     int nthreads() const { return nthr_; }
     void* smem() const { return smem_; }
     void sync() const { blk_->arrive_and_wait(); }
+    void lds_sync() const { blk_->arrive_and_wait(); }
     void wave_sync() const { waves_[tid_ >> 6]->arrive_and_wait(); }
-    uint32_t push(uint32_t acc, bool bit) const { return acc + acc + (uint32_t)bit; }
+    uint32_t push_sign(uint32_t acc, float d) const
+    {
+        uint32_t b;
+        std::memcpy(&b, &d, 4);
+        return (acc << 1) | (b >> 31);
+    }
+    float fmin(float x, float y) const { return std::fmin(x, y); }
+    uint32_t readlane(uint32_t v, int l) const
+    {
+        const int w = tid_ >> 6;
+        xch_[tid_] = v;
+        waves_[w]->arrive_and_wait();
+        const uint32_t r = xch_[w * 64 + l];
+        waves_[w]->arrive_and_wait();
+        return r;
+    }
+    // the GPU copy is asynchronous; here it completes at once
+    void load16(const uint32_t* src, uint32_t* lds_wave_base) const
+    {
+        std::memcpy(lds_wave_base + 4 * (tid_ & 63), src, 16);
+    }
+    template <int N>
+    void wait_loads() const {}
 };
 
-template <int NU, int MD>
+constexpr int kLdsMax = 160 * 1024;  // gfx950 LDS per workgroup
+
+template <int NU, int MD, int NL>
 static int run(const TcqArgs& a)
 {
-    const Smem L = smem_layout<NU, MD>(a.T, a.G, a.nl, a.Gfull, a.sub);
-    constexpr int WCH = Mode<NU, MD>::FG == 1 ? 4 : 1;
-    if (WCH * a.G * Mode<NU, MD>::NW * 64 * 4 > L.gsel - L.exch) return -1;
-    if (L.total > 160 * 1024) return -1;
+    const Smem L = smem_layout<NU, MD, NL>(a.T, a.G, a.Gfull, a.sub, kLdsMax);
+    if (L.total > kLdsMax) return -1;
     const int nthr = 64 * a.G;
     std::vector<char> smem(L.total + 64);
     for (int n = 0; n < a.N; n++) {
@@ -50,11 +77,12 @@ static int run(const TcqArgs& a)
             wv.emplace_back(new std::barrier<>(64));
             ptrs.push_back(wv.back().get());
         }
+        std::vector<uint32_t> xch(nthr);
         std::vector<std::thread> th;
         for (int t = 0; t < nthr; t++) {
             th.emplace_back([&, t]() {
-                CpuX x{t, n, nthr, smem.data(), &blk, ptrs.data()};
-                tcq_tile<NU, MD>(a, x);
+                CpuX x{t, n, nthr, smem.data(), &blk, ptrs.data(), xch.data()};
+                tcq_tile<NU, MD, NL>(a, x, kLdsMax);
             });
         }
         for (auto& t : th) t.join();
@@ -79,9 +107,18 @@ extern "C" int tcq_viterbi_emu(const float* x, const float* w, const float* tab,
     if (S == 256 && T < 8) return -1;
     TcqArgs a{x, w, tab, gains, rec, bp, gsel, init_st, end_st, tab_hi, gains_hi, gcand, best, code, mid_st,
               mid_t, tail, N, T, S, U, G, Gfull, m, sub, U_hi, mix, m2, m3, m4, nl, ld, rot, pbits, pp};
-    if (S == 256) return run<8, 0>(a);
-    if (pp == 0) return run<10, 0>(a);
-    if (pp == 1) return run<10, 1>(a);
-    if (pp == 2) return run<10, 2>(a);
-    return run<10, 3>(a);
+    if (S == 256) return run<8, 0, 4>(a);
+    auto by_nl = [&](auto md) -> int {
+        constexpr int MD = decltype(md)::value;
+        switch (nl) {
+            case 4: return run<10, MD, 4>(a);
+            case 8: return run<10, MD, 8>(a);
+            case 16: return run<10, MD, 16>(a);
+            default: return run<10, MD, 32>(a);
+        }
+    };
+    if (pp == 0) return by_nl(std::integral_constant<int, 0>{});
+    if (pp == 1) return by_nl(std::integral_constant<int, 1>{});
+    if (pp == 2) return by_nl(std::integral_constant<int, 2>{});
+    return by_nl(std::integral_constant<int, 3>{});
 }
