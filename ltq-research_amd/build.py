@@ -15,7 +15,8 @@ CSRC = HERE / "csrc"
 OUT = HERE / "ltq_amd" / "libltq_hip.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I", str(CSRC)]
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I", str(CSRC),
+         "-I", str(HERE.parent / "include")]
 
 
 def build(verbose: bool = False) -> Path:

@@ -196,8 +196,11 @@ LTQ_HD Smem smem_layout(int T, int G, int Gfull, int sub, int lds_max)
     // ring slots: one window of decision words of every gain slot, padded to whole 1 KB wave loads
     L.slot_words = TB::LW * G * 256;
     L.ring = L.exch;
+    // two workgroups per CU (two waves per SIMD) whenever the forward state fits half of the LDS: a single
+    // wave per SIMD issues at most every other VALU cycle, so occupancy is worth more than ring depth
+    const int budget = 2 * fwd_end <= lds_max ? lds_max / 2 : lds_max;
     int ns = 4;
-    while (ns > 2 && L.ring + ns * 4 * L.slot_words > lds_max && L.ring + ns * 4 * L.slot_words > fwd_end) ns--;
+    while (ns > 2 && L.ring + ns * 4 * L.slot_words > budget && L.ring + ns * 4 * L.slot_words > fwd_end) ns--;
     L.nslot = ns;
     const int ring_end = L.ring + ns * 4 * L.slot_words;
     L.total = fwd_end > ring_end ? fwd_end : ring_end;

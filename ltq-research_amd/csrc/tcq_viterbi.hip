@@ -9,6 +9,8 @@
 
 #include "tcq_launch.h"
 
+#include "ltq_hip.h"
+
 namespace ltq {
 
 // instantiated in tcq_inst_*.hip (compiled in parallel)

@@ -19,6 +19,9 @@ SIGNATURES = {
     "tcq_viterbi": (ci, [vp] * 15 + [ci] * 18 + [vp, ci, vp]),
     # src/cuda/tcq_viterbi.cu:806-807; src/tcq_proto.py:531-532
     "lut_subs_quant": (ci, [vp] * 4 + [ci, cf, cf, ci, vp]),
+    # FWHT-256 (src/iqk_format.py:153-170), rows with a fused scale / columns
+    "ltq_fwht256_rows": (ci, [vp, ci, vp, cl, cl, cl, cl, vp, ci, vp]),
+    "ltq_fwht256_cols": (ci, [vp, vp, cl, cl, cl, cl, vp, ci, vp]),
 }
 
 

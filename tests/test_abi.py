@@ -1,0 +1,51 @@
+"""The C ABI: libltq_hip.so loads on a machine without a GPU and exports every function include/*.h declares,
+with the argument counts the Python loader binds (no compute calls here)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declarations():
+    out = {}
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"\bint\s+(\w+)\s*\(([^;{]*)\)\s*;", text):
+            args = [a for a in m.group(2).replace("\n", " ").split(",") if a.strip() and a.strip() != "void"]
+            out[m.group(1)] = len(args)
+    return out
+
+
+def test_header_declares_entry_points():
+    decl = _declarations()
+    assert {"tcq_viterbi", "ltq_fwht256_rows", "ltq_fwht256_cols"} <= set(decl)
+    assert decl["tcq_viterbi"] == 36  # the reference's ctypes binding: 15 pointers, 18 ints, pbits, pp, stream
+
+
+def test_library_exports_every_declared_symbol():
+    from ltq_amd import _lib
+    so = ROOT / "ltq-research_amd" / "ltq_amd" / "libltq_hip.so"
+    if not so.exists():
+        pytest.skip("libltq_hip.so not built (run __graft_entry__.build())")
+    L = ctypes.CDLL(str(so))
+    for name, nargs in _declarations().items():
+        assert hasattr(L, name), f"{name} declared in include/ but not exported"
+        assert name in _lib.SIGNATURES, f"{name} not bound by ltq_amd._lib"
+        assert len(_lib.SIGNATURES[name][1]) == nargs, name
+
+
+def test_product_path_fails_loudly_without_device():
+    """No CPU fallback: on a machine without a HIP device every kernel entry raises."""
+    torch = pytest.importorskip("torch")
+    if torch.cuda.is_available():
+        pytest.skip("a device is present")
+    from ltq_amd import _lib
+    from ltq_amd.rotation import fwht_rows
+    from ltq_amd.tcq_proto import viterbi_ub_cuda
+    with pytest.raises(_lib.LtqLibraryMissing):
+        fwht_rows(torch.zeros((1, 256)))
+    with pytest.raises(_lib.LtqLibraryMissing):
+        viterbi_ub_cuda(torch.zeros((1, 32)), torch.zeros(16), 3, 10, 359)
