@@ -134,6 +134,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample (0 = skip)")
     ap.add_argument("--blocks", type=int, default=0, help="column blocks per step (0 = all 56; profiling runs only)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="profiling runs: first copy this many MiB device-to-device (a known-size kernel that "
+                         "calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the Viterbi path is row-sharded with no exchange on the hot path, "
@@ -148,6 +151,11 @@ def main():
     torch.cuda.set_device(dev)
     cfg = TCQ_CONFIG[FORMAT]
     f = make_format(FORMAT)
+    if args.copy_mib:
+        a = torch.ones(args.copy_mib << 18, device=dev)
+        torch.empty_like(a).copy_(a)
+        torch.cuda.synchronize()
+        del a
     tiles, wts = prepare(dev)
     nblk = args.blocks or tiles.shape[0]
     lut = torch.tensor(f.lut, device=dev)
