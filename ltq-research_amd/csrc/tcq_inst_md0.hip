@@ -1,8 +1,13 @@
-// Instantiations of the Viterbi launcher for parity mode 0 (S = 1024, every label count).
+// Instantiations of the Viterbi launcher for parity mode 0 (S = 1024; 4 states per lane for G <= 4,
+// 8 for G = 8; every label count).
 #include "tcq_launch.h"
 namespace ltq {
-template int launch<10, 0, 4>(const TcqArgs&, hipStream_t);
-template int launch<10, 0, 8>(const TcqArgs&, hipStream_t);
-template int launch<10, 0, 16>(const TcqArgs&, hipStream_t);
-template int launch<10, 0, 32>(const TcqArgs&, hipStream_t);
+template int launch<10, 2, 0, 4>(const TcqArgs&, hipStream_t);
+template int launch<10, 2, 0, 8>(const TcqArgs&, hipStream_t);
+template int launch<10, 2, 0, 16>(const TcqArgs&, hipStream_t);
+template int launch<10, 2, 0, 32>(const TcqArgs&, hipStream_t);
+template int launch<10, 3, 0, 4>(const TcqArgs&, hipStream_t);
+template int launch<10, 3, 0, 8>(const TcqArgs&, hipStream_t);
+template int launch<10, 3, 0, 16>(const TcqArgs&, hipStream_t);
+template int launch<10, 3, 0, 32>(const TcqArgs&, hipStream_t);
 }  // namespace ltq

@@ -1,8 +1,13 @@
-// Instantiations of the Viterbi launcher for parity mode 1 (S = 1024, every label count).
+// Instantiations of the Viterbi launcher for parity mode 1 (S = 1024; 4 states per lane for G <= 4,
+// 8 for G = 8; every label count).
 #include "tcq_launch.h"
 namespace ltq {
-template int launch<10, 1, 4>(const TcqArgs&, hipStream_t);
-template int launch<10, 1, 8>(const TcqArgs&, hipStream_t);
-template int launch<10, 1, 16>(const TcqArgs&, hipStream_t);
-template int launch<10, 1, 32>(const TcqArgs&, hipStream_t);
+template int launch<10, 2, 1, 4>(const TcqArgs&, hipStream_t);
+template int launch<10, 2, 1, 8>(const TcqArgs&, hipStream_t);
+template int launch<10, 2, 1, 16>(const TcqArgs&, hipStream_t);
+template int launch<10, 2, 1, 32>(const TcqArgs&, hipStream_t);
+template int launch<10, 3, 1, 4>(const TcqArgs&, hipStream_t);
+template int launch<10, 3, 1, 8>(const TcqArgs&, hipStream_t);
+template int launch<10, 3, 1, 16>(const TcqArgs&, hipStream_t);
+template int launch<10, 3, 1, 32>(const TcqArgs&, hipStream_t);
 }  // namespace ltq

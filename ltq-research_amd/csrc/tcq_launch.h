@@ -1,10 +1,10 @@
 // gfx950 launch plumbing for the TCQ Viterbi kernel: the wavefront primitives the portable body uses, the
 // __global__ entry and a launcher. Each tcq_inst_*.hip instantiates the launcher for one parity mode, so the
-// 17 (S, mode, label-count) variants compile in parallel.
+// variants compile in parallel.
 #pragma once
 #include <hip/hip_runtime.h>
 
-#include "tcq_kernel.h"
+#include "tcq_trellis.h"
 
 namespace ltq {
 
@@ -26,21 +26,18 @@ struct GpuX {
         __builtin_amdgcn_s_barrier();
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
-    __device__ __forceinline__ void wave_sync() const
-    {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
     // acc = 2 * acc + sign bit of d (v_alignbit_b32 acc, acc, d, 31)
     __device__ __forceinline__ uint32_t push_sign(uint32_t acc, float d) const
     {
         return __builtin_amdgcn_alignbit(acc, __builtin_bit_cast(uint32_t, d), 31);
     }
     __device__ __forceinline__ float fmin(float x, float y) const { return __builtin_fminf(x, y); }
-    __device__ __forceinline__ uint32_t readlane(uint32_t v, int l) const
+    __device__ __forceinline__ float shfl_xor(float v, int m) const { return __shfl_xor(v, m, 64); }
+    __device__ __forceinline__ int shfl_xor(int v, int m) const { return __shfl_xor(v, m, 64); }
+    // a value every lane of the wave holds: kept in a scalar register
+    __device__ __forceinline__ uint32_t uniform(uint32_t v) const
     {
-        return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+        return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
     }
     // asynchronous 16-byte copy global -> LDS; lane l's bytes land at lds_wave_base + 16 l
     __device__ __forceinline__ void load16(const uint32_t* src, uint32_t* lds_wave_base) const
@@ -48,45 +45,47 @@ struct GpuX {
         __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)lds_wave_base,
                                          16, 0, 0);
     }
-    template <int N>
-    __device__ __forceinline__ void wait_loads() const
+    // at most n (<= 15) of this wave's vector memory operations still outstanding
+    __device__ __forceinline__ void wait_loads(int n) const
     {
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0xF70);  // vmcnt(N) only
+        switch (n) {
+#define LTQ_W(k) \
+    case k: __builtin_amdgcn_s_waitcnt(k | 0xF70); break;
+            LTQ_W(1) LTQ_W(2) LTQ_W(3) LTQ_W(4) LTQ_W(5) LTQ_W(6) LTQ_W(7) LTQ_W(8) LTQ_W(9) LTQ_W(10) LTQ_W(11)
+            LTQ_W(12) LTQ_W(13) LTQ_W(14) LTQ_W(15)
+#undef LTQ_W
+            default: __builtin_amdgcn_s_waitcnt(0xF70); break;  // vmcnt(0)
+        }
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
 };
 
-// WG = most wavefronts (gain slots) per workgroup the instance serves: 4 lets the compiler use the whole
-// 512-entry register file of a SIMD (one wave per SIMD), 8 halves it.
-template <int NU, int MD, int NL, int WG>
-__global__ __launch_bounds__(64 * WG) void tcq_viterbi_kernel(TcqArgs a, int lds_max)
+// Up to 16 wavefronts (1024 threads): G gain slots x Q waves.
+template <int NU, int RB, int MD, int NL>
+__global__ __launch_bounds__(1024) void tcq_viterbi_kernel(TcqArgs a, int lds_max)
 {
     GpuX x;
-    tcq_tile<NU, MD, NL>(a, x, lds_max);
+    tcq_tile<NU, RB, MD, NL>(a, x, lds_max);
 }
 
 int device_lds_max();
 
-template <int NU, int MD, int NL>
+template <int NU, int RB, int MD, int NL>
 int launch(const TcqArgs& a, hipStream_t stream)
 {
     const int lds_max = device_lds_max();
     if (lds_max <= 0) return -1;
-    const Smem L = smem_layout<NU, MD, NL>(a.T, a.G, a.Gfull, a.sub, lds_max);
+    const Smem L = smem_layout<NU, RB, MD, NL>(a.T, a.G, a.Gfull, a.sub, lds_max);
     if (L.total > lds_max) return -1;
     static bool attr = false;
     if (!attr) {
-        (void)hipFuncSetAttribute((const void*)tcq_viterbi_kernel<NU, MD, NL, 4>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
-        (void)hipFuncSetAttribute((const void*)tcq_viterbi_kernel<NU, MD, NL, 8>,
+        (void)hipFuncSetAttribute((const void*)tcq_viterbi_kernel<NU, RB, MD, NL>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
         attr = true;
     }
-    if (a.G <= 4)
-        hipLaunchKernelGGL((tcq_viterbi_kernel<NU, MD, NL, 4>), dim3(a.N), dim3(64 * a.G), L.total, stream, a, lds_max);
-    else
-        hipLaunchKernelGGL((tcq_viterbi_kernel<NU, MD, NL, 8>), dim3(a.N), dim3(64 * a.G), L.total, stream, a, lds_max);
+    const int threads = 64 * a.G * Geo<NU, RB>::Q;
+    hipLaunchKernelGGL((tcq_viterbi_kernel<NU, RB, MD, NL>), dim3(a.N), dim3(threads), L.total, stream, a, lds_max);
     return 0;
 }
 

@@ -1,0 +1,961 @@
+// Portable body of the MI355X TCQ Viterbi kernel (one workgroup per 256-weight tile).
+//
+// The same source is compiled two ways:
+//   - for gfx950 by tcq_viterbi.hip (X = GpuX: threadIdx, s_barrier, LDS, v_alignbit decision packing);
+//   - for the host by the CPU emulation used in tests (X = CpuX: one std::thread per lane, barriers),
+//     so layout / indexing bugs show up on the CPU, under AddressSanitizer, before any GPU run.
+//
+// Semantics follow the reference kernel (src/cuda/tcq_viterbi.cu:97-683): Ungerboeck trellis with
+// S = 2^NU states, predecessors p_h = h*S/2 + (s >> 1), labels from parities of (s >> 1) & masks, joint gain
+// slots with a sub-block gain merge, integer / D2 (pp=1) / D4 (pp=2) / EQ (pp=3) parity modes, gain
+// candidates, free / given start, tail-biting end, mid-state pass, cyclic shift, traceback and reconstruction.
+// Ties: strict "<" everywhere, predecessor p0, lowest gain slot, lowest (g, s) index, lowest class / low bit,
+// lowest u -- identical choices to the reference given identical fp32 inputs.
+//
+// MI355X mapping:
+//   - a tile's G gain slots each own Q = S / (64 R) wavefronts; a lane holds R = 4 (R = 8 when G = 8) path
+//     metrics, so G = 4 gives 16 wavefronts: four per SIMD, enough to hide LDS and VALU latency.
+//   - a "phase" is two trellis steps done in registers as one radix-4 block per 4 slots. Between phases the
+//     metrics go through LDS in natural state order (one 16-byte store per block, one 4-byte load per slot,
+//     both conflict-free) and come back in the phase-start layout
+//         state = (r << (6 + QB)) | (q << 6) | lane        (r: register slot, q: wave of the gain slot)
+//     so each lane's states, labels and metric-table offsets are the same in every phase.
+//   - labels are linear over GF(2) in the state bits, so a lane's label for (phase step, slot) is a per-lane
+//     constant XOR; branch metrics E[g][step][label][class] are tabulated per 16-step chunk by all threads
+//     and read with one LDS load per (slot, step).
+//   - decisions: one bit per compare-select -- the sign bit of the difference of the two candidates --
+//     shifted into 32-bit words with v_alignbit (acc = 2 acc + bit), stored per chunk per lane into the
+//     caller's bp / pbits scratch.
+//   - traceback: wavefront 0 walks one phase (two steps) per LDS lookup with its state in scalar registers;
+//     the decision words of the chunks ahead are copied global -> LDS asynchronously by every wavefront.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#ifndef LTQ_DEV
+#define LTQ_DEV __device__ __forceinline__
+#endif
+#ifndef LTQ_HD
+#define LTQ_HD __host__ __device__ __forceinline__
+#endif
+
+namespace ltq {
+
+constexpr float kSent = 3.4e38f;
+constexpr int kMaxG = 16, kMaxU = 128, kMaxSubs = 32, kMaxT = 512;
+
+// Arguments of the reference C ABI tcq_viterbi (tcq_viterbi.cu:743-746), same meaning.
+struct TcqArgs {
+    const float* x;        // [N, ld]
+    const float* w;        // [N, ld]
+    const float* tab;      // [nl * U]
+    const float* gains;    // [Gfull]
+    float* rec;            // [N, ld]
+    uint32_t* bp;          // scratch (caller-allocated, reference size [N, T, G, S/32] u32)
+    uint8_t* gsel;         // scratch, unused here (gain-merge choices stay in LDS)
+    const int* init_st;    // [N] or null
+    int* end_st;           // [N] or null
+    const float* tab_hi;   // [nl * U_hi]
+    const float* gains_hi; // [Gfull]
+    uint8_t* gcand;        // [N, T/sub, G] or null
+    int* best;             // [N]
+    int* code;             // [N, ld] or null
+    int* mid_st;           // [N] or null
+    int mid_t, tail, N, T, S, U, G, Gfull, m, sub, U_hi, mix, m2, m3, m4, nl, ld, rot;
+    uint32_t* pbits;       // scratch (reference size [N, T/2, G, S/32] for pp=1, [N, T/4, G, 9, S/32] for pp>=2)
+    int pp;
+};
+
+LTQ_DEV int parity32(uint32_t v) { return __builtin_popcount(v) & 1; }
+
+// label of state s: (s & 1) | par((s>>1)&m) << 1 | par((s>>1)&m2) << 2 | ... (tcq_viterbi.cu:85-95)
+struct Masks {
+    int m, m2, m3, m4, nl;
+    LTQ_HD int label(int s) const
+    {
+        int lb = (__builtin_popcount((uint32_t)((s >> 1) & m)) & 1) << 1 | (s & 1);
+        if (nl >= 8) lb |= (__builtin_popcount((uint32_t)((s >> 1) & m2)) & 1) << 2;
+        if (nl >= 16) lb |= (__builtin_popcount((uint32_t)((s >> 1) & m3)) & 1) << 3;
+        if (nl >= 32) lb |= (__builtin_popcount((uint32_t)((s >> 1) & m4)) & 1) << 4;
+        return lb;
+    }
+};
+
+// Geometry: NU state bits = RB register bits (top) + QB wave bits + 6 lane bits at a phase start.
+template <int NU, int RB>
+struct Geo {
+    static constexpr int S = 1 << NU, HALF = S / 2, R = 1 << RB, NB = R / 4, QB = NU - 6 - RB, Q = 1 << QB;
+    static_assert(RB >= 2 && QB >= 0, "geometry");
+    // state of register slot r of (wave q, lane l) at a phase start
+    static LTQ_HD int start(int r, int q, int l) { return (r << (6 + QB)) | (q << 6) | l; }
+    // state after step a of block b, slot jj = 2 ca + e (e: the block's second input bit)
+    static LTQ_HD int mid(int b, int jj, int q, int l)
+    {
+        return ((jj & 1) << (NU - 1)) | (b << (7 + QB)) | (q << 7) | (l << 1) | (jj >> 1);
+    }
+    // state after step b of block b, output j = 2 ca + cb
+    static LTQ_HD int end(int b, int j, int q, int l) { return (b << (8 + QB)) | (q << 8) | (l << 2) | j; }
+};
+
+// Decision-bit layout per parity mode (MD: 0 integer, 1 D2, 2 D4, 3 EQ). Phase types: 0 (integer pair,
+// D2 pair, D4 / EQ phase A) and 1 (D4 / EQ phase B); D4 / EQ alternate A, B from step 0.
+template <int MD, int RB>
+struct Md {
+    static constexpr int NB = (1 << RB) / 4, NP = MD ? 2 : 1, XF = MD >= 2 ? 2 : 1;
+    static constexpr bool TWO = MD >= 2;
+    static constexpr int PBLK(int pt) { return MD == 0 ? 4 : MD == 1 ? 10 : MD == 2 ? (pt ? 24 : 14) : (pt ? 12 : 6); }
+    static constexpr int PPH(int pt) { return NB * PBLK(pt); }
+    static constexpr int NPC = (MD == 1 && NB == 1) ? 16 : 8;   // phases per chunk
+    static constexpr int CK = 2 * NPC;                          // steps per chunk
+    static constexpr int PT(int pi) { return TWO ? (pi & 1) : 0; }
+    // pushes before in-chunk phase pi
+    static constexpr int OFF(int pi) { return TWO ? (pi / 2) * (PPH(0) + PPH(1)) + (pi & 1) * PPH(0) : pi * PPH(0); }
+    static constexpr int CB = OFF(NPC);       // pushes per full chunk
+    static constexpr int NW = (CB + 31) / 32; // words per lane per chunk
+    static constexpr int LAST = CB - 32 * (NW - 1);
+};
+
+LTQ_HD int align16(int v) { return (v + 15) & ~15; }
+
+struct alignas(16) F4 {
+    float x, y, z, w;
+};
+
+// dynamic LDS layout (byte offsets), identical on host (launch size) and device
+struct Smem {
+    int x, w, tab, tab_hi, gain, gain_hi, gc, ce, gix, gsel, st, g, par, red, ctl, tabs, exch, total;
+    int tab_floats;   // one chunk table (all gain slots)
+    int exch_floats;  // one exchange buffer (all gain slots)
+    int dbl;          // exchange double-buffered
+    int ring, nslot, slot_words;  // traceback ring (overlaps tables + exchange, dead after the forward pass)
+};
+
+template <int NU, int RB, int MD, int NL>
+LTQ_HD Smem smem_layout(int T, int G, int Gfull, int sub, int lds_max)
+{
+    using GE = Geo<NU, RB>;
+    using MM = Md<MD, RB>;
+    Smem L;
+    int o = 0;
+    const int nsub = T / sub;
+    L.x = o; o = align16(o + 4 * T);
+    L.w = o; o = align16(o + 4 * T);
+    L.tab = o; o = align16(o + 4 * 4 * kMaxU);
+    L.tab_hi = o; o = align16(o + 4 * 4 * kMaxU);
+    L.gain = o; o = align16(o + 4 * kMaxG);
+    L.gain_hi = o; o = align16(o + 4 * kMaxG);
+    L.gc = o; o = align16(o + nsub * kMaxG);
+    L.ce = o; o = align16(o + 4 * nsub * kMaxG);
+    L.gix = o; o = align16(o + T * G);                     // gain index per (step, slot); bit 7: hi table
+    L.gsel = o; o = align16(o + (G > 1 ? nsub * GE::S : 0));
+    L.st = o; o = align16(o + 2 * T + 32);
+    L.g = o; o = align16(o + T + 32);
+    L.par = o; o = align16(o + T + 32);
+    L.red = o; o = align16(o + 8 * 64);
+    L.ctl = o; o = align16(o + 4 * 8);
+    L.tab_floats = G * MM::CK * NL * MM::NP;
+    L.exch_floats = G * MM::XF * GE::S;
+    L.tabs = o;
+    L.exch = align16(L.tabs + 2 * 4 * L.tab_floats);
+    const int one = align16(L.exch + 4 * L.exch_floats), two = align16(L.exch + 2 * 4 * L.exch_floats);
+    L.dbl = two <= lds_max ? 1 : 0;
+    const int fwd_end = L.dbl ? two : one;
+    // ring slots: one chunk of decision words of every (gain slot, wave, lane), whole 1 KB wave loads + pad
+    const int cw = G * GE::Q * 64 * MM::NW;
+    L.slot_words = ((cw + 255) / 256) * 256 + 256;
+    L.ring = L.tabs;
+    int ns = 4;
+    while (ns > 2 && L.ring + ns * 4 * L.slot_words > lds_max && L.ring + ns * 4 * L.slot_words > fwd_end) ns--;
+    L.nslot = ns;
+    const int ring_end = L.ring + ns * 4 * L.slot_words;
+    L.total = fwd_end > ring_end ? fwd_end : ring_end;
+    return L;
+}
+
+// words of decision scratch of one tile available in bp + pbits
+LTQ_HD long scratch_words(int T, int G, int S, int pp)
+{
+    const long bp = (long)T * G * (S / 32);
+    const long pb = pp == 1 ? (long)(T / 2) * G * (S / 32) : pp >= 2 ? (long)(T / 4) * G * 9 * (S / 32) : 0;
+    return bp + pb;
+}
+
+// words of decision scratch one tile needs (full chunks of NW words per lane, the last chunk only the words
+// holding its real decisions)
+template <int NU, int RB, int MD>
+LTQ_HD long needed_words(int T, int G)
+{
+    using MM = Md<MD, RB>;
+    const int nph = T / 2, full = nph / MM::NPC, rem = nph % MM::NPC;
+    const int rbits = MM::TWO ? (rem / 2) * (MM::PPH(0) + MM::PPH(1)) + (rem & 1) * MM::PPH(0) : rem * MM::PPH(0);
+    const long w = (long)full * MM::NW + (rbits + 31) / 32;
+    return w * G * Geo<NU, RB>::Q * 64;
+}
+
+// squared-error minimum over levels u0, u0+du, ... < Ut of fl(x - fl(g * tab[u]))^2 (tcq_viterbi.cu:46-54, 75-83)
+LTQ_DEV float level_err(float xt, float gain, const float* tb, int u0, int Ut, int du)
+{
+    float e = kSent;
+    for (int u = u0; u < Ut; u += du) {
+        const float v = gain * tb[u];
+        const float d = xt - v;
+        const float dd = d * d;
+        e = dd < e ? dd : e;
+    }
+    return e;
+}
+
+// Compare-select-push: for candidates (x, y) with "x wins when x < y" the kernel computes
+//   m = min(x, y)          (v_min_f32: equals x < y ? x : y)
+//   d = x - y              (sign bit = [x < y]: no metric is -0, NaN or infinite)
+//   acc = 2 acc + sign(d)  (v_alignbit_b32 acc, acc, d, 31)
+#define LTQ_CSP(P, x, y, m)                                         \
+    do {                                                            \
+        const float d_ = (x) - (y);                                 \
+        m = X_.fmin((x), (y));                                      \
+        acc[(P) >> 5] = X_.push_sign(acc[(P) >> 5], d_);            \
+    } while (0)
+#define LTQ_PUSH0(P) acc[(P) >> 5] = X_.push_sign(acc[(P) >> 5], 0.f)
+
+// ------------------------------------------------------------------------------------------------
+// One radix-4 block of a phase (two trellis steps). Inputs: slot j = 2 hbit + lbit (hbit: the state's top
+// bit, consumed by step a; lbit: consumed by step b). Step a: butterflies (e, 2+e) -> intermediate slot
+// jj = 2 ca + e; step b: butterflies (2f, 2f+1) -> output j = 2 f + cb with f = ca. The predecessor with the
+// high state bit wins only when strictly smaller (p0 on ties), as in the reference.
+// ma[jj][p]: metric of intermediate jj (step a), mb[j][p]: metric of output j (step b), p = parity class.
+// ------------------------------------------------------------------------------------------------
+template <int MD, int PT, int P0, class X>
+LTQ_DEV void run_block(bool init, const bool (&ok)[4], const float (&I)[2][4], const float (&ma)[4][2],
+                       const float (&mb)[4][2], float (&O)[2][4], uint32_t* acc, X& X_)
+{
+    constexpr bool EQ = MD == 3;
+    if constexpr (MD == 0) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int j0 = e, j1 = 2 + e;
+            if (init) {
+                v[j0] = ok[j0] ? ma[j0][0] : kSent;
+                v[j1] = ok[j1] ? ma[j1][0] : kSent;
+                LTQ_PUSH0(P0 + e);
+            } else {
+                float m;
+                LTQ_CSP(P0 + e, I[0][j1], I[0][j0], m);
+                v[j0] = m + ma[j0][0];
+                v[j1] = m + ma[j1][0];
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+            const int j0 = 2 * f, j1 = 2 * f + 1;
+            float m;
+            LTQ_CSP(P0 + 2 + f, v[j1], v[j0], m);
+            O[0][j0] = m + mb[j0][0];
+            O[0][j1] = m + mb[j1][0];
+        }
+    } else if constexpr (PT == 0) {
+        // D2 pair, or phase A of a D4 / EQ group: intermediates per low bit b of the first sample
+        float I0[4], I1[4];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int j0 = e, j1 = 2 + e;
+            if (init) {
+#pragma unroll
+                for (int qq = 0; qq < 2; qq++) {
+                    const int jj = qq ? j1 : j0;
+                    I0[jj] = ok[jj] ? ma[jj][0] : kSent;
+                    I1[jj] = ok[jj] ? ma[jj][1] : kSent;
+                }
+                LTQ_PUSH0(P0 + e);
+            } else {
+                float m;
+                LTQ_CSP(P0 + e, I[0][j1], I[0][j0], m);
+                I0[j0] = m + ma[j0][0];
+                I1[j0] = m + ma[j0][1];
+                I0[j1] = m + ma[j1][0];
+                I1[j1] = m + ma[j1][1];
+            }
+        }
+        constexpr int PB = MD == 1 ? 4 : MD == 2 ? 6 : 2;
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+            const int j0 = 2 * f, j1 = 2 * f + 1, PF = P0 + 2 + f * PB;
+            float m0, m1;
+            LTQ_CSP(PF + 0, I0[j1], I0[j0], m0);
+            LTQ_CSP(PF + 1, I1[j1], I1[j0], m1);
+            if constexpr (MD == 1) {  // D2: best class p of the pair (ties: p = 0)
+#pragma unroll
+                for (int qq = 0; qq < 2; qq++) {
+                    const int r = qq ? j1 : j0;
+                    float o;
+                    LTQ_CSP(PF + 2 + qq, m1 + mb[r][1], m0 + mb[r][0], o);
+                    O[0][r] = o;
+                }
+            } else if constexpr (!EQ) {  // D4 phase A: per class c the best b (ties: b = 0), parity b ^ c
+#pragma unroll
+                for (int qq = 0; qq < 2; qq++) {
+                    const int r = qq ? j1 : j0;
+                    float o0, o1;
+                    LTQ_CSP(PF + 2 + 2 * qq + 0, m1 + mb[r][1], m0 + mb[r][0], o0);
+                    LTQ_CSP(PF + 2 + 2 * qq + 1, m1 + mb[r][0], m0 + mb[r][1], o1);
+                    O[0][r] = o0;
+                    O[1][r] = o1;
+                }
+            } else {  // EQ phase A: class c keeps b = c
+#pragma unroll
+                for (int qq = 0; qq < 2; qq++) {
+                    const int r = qq ? j1 : j0;
+                    O[0][r] = m0 + mb[r][0];
+                    O[1][r] = m1 + mb[r][1];
+                }
+            }
+        }
+    } else if constexpr (!EQ) {
+        // D4 phase B: J[c][b] = min over predecessors of C_c + E(b); output = best (c, b) in order 00,01,10,11
+        float J[4][4];  // [2c+b][jj]
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int j0 = e, j1 = 2 + e;
+            float mc0, mc1;
+            LTQ_CSP(P0 + 2 * e + 0, I[0][j1], I[0][j0], mc0);
+            LTQ_CSP(P0 + 2 * e + 1, I[1][j1], I[1][j0], mc1);
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++) {
+                const int jj = qq ? j1 : j0;
+                J[0][jj] = mc0 + ma[jj][0];
+                J[1][jj] = mc0 + ma[jj][1];
+                J[2][jj] = mc1 + ma[jj][0];
+                J[3][jj] = mc1 + ma[jj][1];
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+            const int j0 = 2 * f, j1 = 2 * f + 1, PF = P0 + 4 + f * 10;
+            float mm[4];
+#pragma unroll
+            for (int cb = 0; cb < 4; cb++) LTQ_CSP(PF + cb, J[cb][j1], J[cb][j0], mm[cb]);
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++) {
+                const int r = qq ? j1 : j0;
+                float v = mm[0] + mb[r][0];
+                LTQ_CSP(PF + 4 + 3 * qq + 0, mm[1] + mb[r][1], v, v);
+                LTQ_CSP(PF + 4 + 3 * qq + 1, mm[2] + mb[r][1], v, v);
+                LTQ_CSP(PF + 4 + 3 * qq + 2, mm[3] + mb[r][0], v, v);
+                O[0][r] = v;
+            }
+        }
+    } else {
+        // EQ phase B: classes keep b = c; output = best class (ties: c = 0)
+        float Jc[2][4];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int j0 = e, j1 = 2 + e;
+            float mc0, mc1;
+            LTQ_CSP(P0 + 2 * e + 0, I[0][j1], I[0][j0], mc0);
+            LTQ_CSP(P0 + 2 * e + 1, I[1][j1], I[1][j0], mc1);
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++) {
+                const int jj = qq ? j1 : j0;
+                Jc[0][jj] = mc0 + ma[jj][0];
+                Jc[1][jj] = mc1 + ma[jj][1];
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+            const int j0 = 2 * f, j1 = 2 * f + 1, PF = P0 + 4 + f * 4;
+            float m0, m1;
+            LTQ_CSP(PF + 0, Jc[0][j1], Jc[0][j0], m0);
+            LTQ_CSP(PF + 1, Jc[1][j1], Jc[1][j0], m1);
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++) {
+                const int r = qq ? j1 : j0;
+                float o;
+                LTQ_CSP(PF + 2 + qq, m1 + mb[r][1], m0 + mb[r][0], o);
+                O[0][r] = o;
+            }
+        }
+    }
+}
+
+// Location of decision word (tile n, linear word L): bp holds the first scratch_words(bp part) words of a
+// tile, pbits the rest.
+struct DecMap {
+    uint32_t* bp;
+    uint32_t* pb;
+    long cap_bp;
+    LTQ_DEV uint32_t* at(long L) const { return L < cap_bp ? bp + L : pb + (L - cap_bp); }
+};
+
+// ------------------------------------------------------------------------------------------------
+// The per-tile kernel body.
+// X provides: tid(), wave() (tid / 64, uniform), tile(), nthreads(), smem(), sync() (full barrier incl. global
+// memory), lds_sync() (barrier for LDS only), push_sign(acc, d), fmin(x, y), shfl_xor(v, mask) (within a
+// wavefront), uniform(v) (value of lane 0), load16(global src, LDS wave base) (asynchronous 16-byte
+// global -> LDS copy landing at base + 16 * lane), wait_loads(n) (at most n such copies of this wave still
+// outstanding, n <= 15).
+// ------------------------------------------------------------------------------------------------
+template <int NU, int RB, int MD, int NL, class X>
+LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
+{
+    using GE = Geo<NU, RB>;
+    using MM = Md<MD, RB>;
+    constexpr int S = GE::S, HALF = GE::HALF, R = GE::R, NB = GE::NB, QB = GE::QB, Q = GE::Q;
+    constexpr int NP = MM::NP, NPC = MM::NPC, CK = MM::CK, NW = MM::NW, XF = MM::XF;
+    constexpr bool TWO = MM::TWO, EQ = MD == 3;
+
+    const int n = X_.tile(), tid = X_.tid(), nthr = X_.nthreads();
+    const int lane = tid & 63, wv = X_.wave();
+    const int g = wv / Q, q = wv % Q;  // gain slot and wave of the slot (uniform)
+    const int T = a.T, G = a.G, sub = a.sub, U = a.U, U_hi = a.U_hi, mix = MD ? 0 : a.mix;
+    const int Gf = a.Gfull, nsub = T / sub;
+    const bool cand = a.gcand != nullptr;
+    const Masks mk{a.m, a.m2, a.m3, a.m4, NL};
+    const Smem SM = smem_layout<NU, RB, MD, NL>(T, G, Gf, sub, lds_max);
+    char* sm = (char*)X_.smem();
+    float* s_x = (float*)(sm + SM.x);
+    float* s_w = (float*)(sm + SM.w);
+    float* s_tab = (float*)(sm + SM.tab);
+    float* s_tab_hi = (float*)(sm + SM.tab_hi);
+    float* s_gain = (float*)(sm + SM.gain);
+    float* s_gain_hi = (float*)(sm + SM.gain_hi);
+    uint8_t* s_gc = (uint8_t*)(sm + SM.gc);
+    float* s_ce = (float*)(sm + SM.ce);
+    uint8_t* s_gix = (uint8_t*)(sm + SM.gix);
+    uint8_t* s_gsel = (uint8_t*)(sm + SM.gsel);
+    uint16_t* s_st = (uint16_t*)(sm + SM.st);
+    uint8_t* s_g = (uint8_t*)(sm + SM.g);
+    uint8_t* s_par = (uint8_t*)(sm + SM.par);
+    float* s_rv = (float*)(sm + SM.red);
+    int* s_ri = (int*)(sm + SM.red + 4 * 64);
+    int* s_ctl = (int*)(sm + SM.ctl);
+    float* s_tabs = (float*)(sm + SM.tabs);
+    float* s_exch = (float*)(sm + SM.exch);
+
+    // ---- tile load (tcq_viterbi.cu:133-140) -----------------------------------------------------
+    for (int i = tid; i < T; i += nthr) {
+        const size_t j = (size_t)n * a.ld + (size_t)((i + a.rot) % a.ld);
+        s_x[i] = a.x[j];
+        s_w[i] = a.w[j];
+    }
+    for (int i = tid; i < NL * U; i += nthr) s_tab[i] = a.tab[i];
+    for (int i = tid; i < NL * U_hi; i += nthr) s_tab_hi[i] = a.tab_hi[i];
+    if (tid < Gf) {
+        s_gain[tid] = a.gains[tid];
+        s_gain_hi[tid] = a.gains_hi[tid];
+    }
+    const int s0 = a.init_st ? a.init_st[n] : -1;
+    X_.lds_sync();
+
+    // ---- gain candidates: the G gains of lowest scalar error per sub-block (tcq_viterbi.cu:155-180) ----
+    if (cand) {
+        for (int i = tid; i < nsub * Gf; i += nthr) {
+            const int j = i / Gf, gi = i % Gf;
+            float e = 0.f;
+            for (int t = j * sub; t < (j + 1) * sub; t++) {
+                const bool hi = mix > 0 && ((t / mix) & 1);
+                const float be = hi ? level_err(s_x[t], s_gain_hi[gi], s_tab_hi, 0, NL * U_hi, 1)
+                                    : level_err(s_x[t], s_gain[gi], s_tab, 0, NL * U, 1);
+                const float prod = be * s_w[t];
+                e = e + prod;
+            }
+            s_ce[i] = e;
+        }
+        X_.lds_sync();
+        if (tid < nsub) {
+            uint32_t used = 0;
+            for (int c = 0; c < G; c++) {
+                int bg = 0;
+                float be = kSent;
+                for (int gi = 0; gi < Gf; gi++)
+                    if (!((used >> gi) & 1) && s_ce[tid * Gf + gi] < be) {
+                        be = s_ce[tid * Gf + gi];
+                        bg = gi;
+                    }
+                used |= 1u << bg;
+                s_gc[tid * G + c] = (uint8_t)bg;
+                a.gcand[((size_t)n * nsub + tid) * G + c] = (uint8_t)bg;
+            }
+        }
+        X_.lds_sync();
+    }
+    // gain index of every (step, slot), bit 7 = the step uses the hi table (mix)
+    for (int i = tid; i < T * G; i += nthr) {
+        const int t = i / G, gg = i % G;
+        const int gi = cand ? (int)s_gc[(t / sub) * G + gg] : gg;
+        const bool hi = mix > 0 && ((t / mix) & 1);
+        s_gix[i] = (uint8_t)(gi | (hi ? 0x80 : 0));
+    }
+    X_.lds_sync();
+
+    // metric table of chunk cc -> buffer (cc & 1): E[g][k][label][p] for steps cc*CK + k (0 beyond T)
+    const int TF = SM.tab_floats;
+    auto tables = [&](int cc) {
+        float* tb = s_tabs + (cc & 1) * TF;
+        for (int e = tid; e < TF; e += nthr) {
+            const int p = NP == 2 ? (e & 1) : 0;
+            const int lb = (e / NP) % NL, k = (e / (NP * NL)) % CK, gg = e / (NP * NL * CK);
+            const int t = cc * CK + k;
+            float E = 0.f;
+            if (t < T) {
+                const int gx = s_gix[t * G + gg], gi = gx & 0x7f;
+                float be;
+                if (MD) be = level_err(s_x[t], s_gain[gi], s_tab + lb * U, p, U, 2);
+                else if (gx & 0x80) be = level_err(s_x[t], s_gain_hi[gi], s_tab_hi + lb * U_hi, 0, U_hi, 1);
+                else be = level_err(s_x[t], s_gain[gi], s_tab + lb * U, 0, U, 1);
+                E = be * s_w[t];
+                E = E + 0.0f;  // -0 -> +0: no metric is -0, so sign(x - y) is exactly [x < y]
+            }
+            tb[e] = E;
+        }
+    };
+
+    // ---- per-lane constants: table offsets of each (block, slot) at step a / b, start check -----------
+    const int la_lane = mk.label(GE::mid(0, 0, q, lane)), lb_lane = mk.label(GE::end(0, 0, q, lane));
+    int offa[NB][4], offb[NB][4];
+    bool ok[NB][4];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            offa[b][j] = (g * CK * NL + (la_lane ^ mk.label(GE::mid(b, j, 0, 0)))) * NP;
+            offb[b][j] = (g * CK * NL + (lb_lane ^ mk.label(GE::end(b, j, 0, 0)))) * NP;
+            const int sm1 = GE::mid(b, j, q, lane);
+            ok[b][j] = s0 < 0 || (sm1 >> 1) == (s0 & (HALF - 1));
+        }
+
+    const DecMap dm{a.bp + (size_t)n * T * G * (S / 32),
+                    a.pbits ? a.pbits + (size_t)n * (scratch_words(T, G, S, a.pp) - (long)T * G * (S / 32)) : nullptr,
+                    (long)T * G * (S / 32)};
+    const int nph = T / 2;
+    const int nchunk = (nph + NPC - 1) / NPC;
+    const long chunk_words = (long)G * Q * 64 * NW;
+
+    float I[2][NB][4];  // phase inputs (class planes for phase B)
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) I[c][b][j] = 0.f;
+    float O[2][NB][4];
+    uint32_t acc[NW];
+
+    tables(0);
+    X_.lds_sync();
+    int xph = 0;                         // global phase counter (exchange buffer parity)
+    int next_merge = sub, merge_j = 1;   // next sub-block boundary and its index
+    for (int c = 0; c < nchunk; c++) {
+#pragma unroll
+        for (int w = 0; w < NW; w++) acc[w] = 0;
+        const float* tb = s_tabs + (c & 1) * TF;
+        int real = 0;  // phases of this chunk inside the tile
+#pragma unroll
+        for (int pi = 0; pi < NPC; pi++) {
+            const int ta = c * CK + 2 * pi;
+            if (ta >= T) {  // beyond the tile end: zero pushes keep every decision bit at its fixed position
+#pragma unroll
+                for (int i = 0; i < MM::PPH(MM::PT(pi)); i++) LTQ_PUSH0(MM::OFF(pi) + i);
+                continue;
+            }
+            real++;
+            // metrics of steps ta, ta + 1 for every (block, slot)
+            float ma[NB][4][2], mb[NB][4][2];
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+#pragma unroll
+                    for (int p = 0; p < NP; p++) {
+                        ma[b][j][p] = tb[offa[b][j] + (2 * pi) * NL * NP + p];
+                        mb[b][j][p] = tb[offb[b][j] + (2 * pi + 1) * NL * NP + p];
+                    }
+            const bool init = ta == 0;
+            // run the blocks (compile-time phase type and push offsets)
+#define LTQ_RUN_PHASE(PTv, PIv)                                                                            \
+    do {                                                                                                   \
+        _Pragma("unroll") for (int b = 0; b < NB; b++)                                                     \
+        {                                                                                                  \
+            float Ib[2][4], Ob[2][4];                                                                      \
+            _Pragma("unroll") for (int cc2 = 0; cc2 < 2; cc2++)                                            \
+                _Pragma("unroll") for (int j = 0; j < 4; j++) Ib[cc2][j] = I[cc2][b][j];                   \
+            if (b == 0)                                                                                    \
+                run_block<MD, PTv, MM::OFF(PIv) + 0 * MM::PBLK(PTv)>(init, ok[0], Ib, ma[0], mb[0], Ob, acc, X_); \
+            else                                                                                           \
+                run_block<MD, PTv, MM::OFF(PIv) + 1 * MM::PBLK(PTv)>(init, ok[NB - 1], Ib, ma[NB - 1],     \
+                                                                    mb[NB - 1], Ob, acc, X_);              \
+            _Pragma("unroll") for (int cc2 = 0; cc2 < 2; cc2++)                                            \
+                _Pragma("unroll") for (int j = 0; j < 4; j++) O[cc2][b][j] = Ob[cc2][j];                   \
+        }                                                                                                  \
+    } while (0)
+            switch (pi) {
+                case 0: LTQ_RUN_PHASE(MM::PT(0), 0); break;
+                case 1: LTQ_RUN_PHASE(MM::PT(1), 1); break;
+                case 2: LTQ_RUN_PHASE(MM::PT(2), 2); break;
+                case 3: LTQ_RUN_PHASE(MM::PT(3), 3); break;
+                case 4: LTQ_RUN_PHASE(MM::PT(4), 4); break;
+                case 5: LTQ_RUN_PHASE(MM::PT(5), 5); break;
+                case 6: LTQ_RUN_PHASE(MM::PT(6), 6); break;
+                case 7: LTQ_RUN_PHASE(MM::PT(7), 7); break;
+                case 8: LTQ_RUN_PHASE(MM::PT(8 % NPC), 8 % NPC); break;
+                case 9: LTQ_RUN_PHASE(MM::PT(9 % NPC), 9 % NPC); break;
+                case 10: LTQ_RUN_PHASE(MM::PT(10 % NPC), 10 % NPC); break;
+                case 11: LTQ_RUN_PHASE(MM::PT(11 % NPC), 11 % NPC); break;
+                case 12: LTQ_RUN_PHASE(MM::PT(12 % NPC), 12 % NPC); break;
+                case 13: LTQ_RUN_PHASE(MM::PT(13 % NPC), 13 % NPC); break;
+                case 14: LTQ_RUN_PHASE(MM::PT(14 % NPC), 14 % NPC); break;
+                default: LTQ_RUN_PHASE(MM::PT(15 % NPC), 15 % NPC); break;
+            }
+#undef LTQ_RUN_PHASE
+            const int tn = ta + 2;
+            if (tn >= T) continue;  // last phase: outputs stay in registers for the argmin
+            // ---- exchange into the next phase's start layout (+ gain merge at a sub-block boundary) ----
+            const bool carry2 = TWO && MM::PT(pi) == 0;  // phase A -> B carries two class planes
+            float* xb = s_exch + (SM.dbl ? (xph & 1) : 0) * SM.exch_floats;
+            if (!SM.dbl) X_.lds_sync();  // single buffer: every wave has read the previous exchange
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int cp = 0; cp < (carry2 ? 2 : 1); cp++) {
+                    F4 v4;
+                    v4.x = O[cp][b][0];
+                    v4.y = O[cp][b][1];
+                    v4.z = O[cp][b][2];
+                    v4.w = O[cp][b][3];
+                    *(F4*)(xb + (g * XF + cp) * S + GE::end(b, 0, q, lane)) = v4;
+                }
+            X_.lds_sync();
+            xph++;
+            if (pi == 0 && c + 1 < nchunk) tables(c + 1);  // next chunk's table (its buffer was last read in chunk c-1)
+            const bool at_sub = tn == next_merge;
+            const int jm = merge_j;
+            if (at_sub) {
+                next_merge += sub;
+                merge_j++;
+            }
+            if (G > 1 && at_sub) {
+#pragma unroll
+                for (int b = 0; b < NB; b++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int s = GE::start((j << (RB - 2)) | b, q, lane);
+                        float bv = xb[s];
+                        int bg = 0;
+                        for (int gg = 1; gg < G; gg++) {
+                            const float v = xb[gg * XF * S + s];
+                            if (v < bv) {
+                                bv = v;
+                                bg = gg;
+                            }
+                        }
+                        I[0][b][j] = bv;
+                        if (g == 0) s_gsel[jm * S + s] = (uint8_t)bg;
+                    }
+            } else {
+#pragma unroll
+                for (int cp = 0; cp < (carry2 ? 2 : 1); cp++)
+#pragma unroll
+                    for (int b = 0; b < NB; b++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++)  // slot j of block b is register (j << (RB - 2)) | b
+                            I[cp][b][j] = xb[(g * XF + cp) * S + GE::start((j << (RB - 2)) | b, q, lane)];
+            }
+        }
+        // ---- store this chunk's decision words (left-aligned), only the words holding real bits -------
+        if (MM::LAST < 32) acc[NW - 1] <<= (32 - MM::LAST) & 31;
+        const int rbits = TWO ? (real / 2) * (MM::PPH(0) + MM::PPH(1)) + (real & 1) * MM::PPH(0) : real * MM::PPH(0);
+        const int nwc = real == NPC ? NW : (rbits + 31) / 32;
+        const long L0 = (long)c * chunk_words + ((long)(g * Q + q) * 64 + lane) * nwc;
+#pragma unroll
+        for (int w = 0; w < NW; w++)
+            if (w < nwc) *dm.at(L0 + w) = acc[w];
+    }
+
+    // ---- argmin over (g, s), lowest index on ties (tcq_viterbi.cu:561-578) ---------------------------
+    {
+        const int s_end = a.tail ? s0 : -1;
+        float bv = kSent;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int s = GE::end(b, j, q, lane);
+                const int idx = g * S + s;
+                const float v = (s_end < 0 || s == s_end) ? O[0][b][j] : kSent;
+                if (v < bv || (v == bv && idx < bi)) {
+                    bv = v;
+                    bi = idx;
+                }
+            }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float ov = X_.shfl_xor(bv, off);
+            const int oi = X_.shfl_xor(bi, off);
+            if (ov < bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (lane == 0) {
+            s_rv[wv] = bv;
+            s_ri[wv] = bi;
+        }
+        X_.sync();  // full barrier: also completes every wave's decision-word stores before the traceback
+        if (tid == 0) {
+            const int nw = nthr / 64;
+            float cv = s_rv[0];
+            int ci = s_ri[0];
+            for (int i = 1; i < nw; i++)
+                if (s_rv[i] < cv || (s_rv[i] == cv && s_ri[i] < ci)) {
+                    cv = s_rv[i];
+                    ci = s_ri[i];
+                }
+            if (ci == 0x7fffffff) ci = 0;  // no candidate at or below the sentinel: the reference reads out of range
+            s_ctl[0] = ci;
+        }
+        X_.lds_sync();
+    }
+    const int bi_all = s_ctl[0];
+    // best / end state are stored after the traceback's copies are drained (no global store may sit among the
+    // copies a wave counts with wait_loads)
+    auto store_best = [&]() {
+        if (tid == 0) {
+            a.best[n] = bi_all;
+            if (a.end_st) a.end_st[n] = bi_all % S;
+        }
+    };
+
+    // ---- traceback (tcq_viterbi.cu:601-661) ----------------------------------------------------------
+    // One LDS lookup per phase: the phase's output state names the (wave, lane) that computed it and the
+    // block; that lane's decision bits give the phase's input state, the intermediate state and the parity
+    // classes. Chunks of decision words are copied global -> LDS nslot chunks ahead by every wavefront.
+    {
+        uint32_t* ring = (uint32_t*)(sm + SM.ring);
+        const int nslot = SM.nslot, slot_words = SM.slot_words;
+        const int nwaves = nthr / 64;
+        const uint32_t* dummy = dm.bp;
+        auto chunk_nwc = [&](int cc) {
+            const int rp = (cc + 1) * NPC <= nph ? NPC : nph - cc * NPC;
+            const int rb = TWO ? (rp / 2) * (MM::PPH(0) + MM::PPH(1)) + (rp & 1) * MM::PPH(0) : rp * MM::PPH(0);
+            return rp == NPC ? NW : (rb + 31) / 32;
+        };
+        // loads of one chunk: 16-byte units u = i * 64 + lane for wave loads i = wv, wv + nwaves, ...
+        const int lpw_max = ((G * Q * 16 * NW + 63) / 64 + nwaves - 1) / nwaves;
+        auto issue = [&](int cc) {
+            const int units = G * Q * 16 * chunk_nwc(cc);
+            uint32_t* slot = ring + (cc % nslot) * slot_words;
+            const long base = (long)cc * chunk_words;
+            for (int k = 0; k < lpw_max; k++) {
+                const int i = wv + k * nwaves;
+                const int u = i * 64 + lane;
+                const uint32_t* src = u < units ? dm.at(base + 4L * u) : dummy;
+                if (i * 64 < units) X_.load16(src, slot + i * 256);
+            }
+        };
+        auto loads_of = [&](int cc) {  // wave loads this wave issues for chunk cc
+            const int units = G * Q * 16 * chunk_nwc(cc);
+            int k = 0;
+            for (int kk = 0; kk < lpw_max; kk++)
+                if ((wv + kk * nwaves) * 64 < units) k++;
+            return k;
+        };
+        for (int j = 0; j < nslot; j++)
+            if (nchunk - 1 - j >= 0) issue(nchunk - 1 - j);
+        int st = bi_all % S, gs = bi_all / S, cstar = 0;
+        bool hit = false;
+        const int midpos = a.mid_st ? a.mid_t - 1 : -1;
+        int nbnd = ((T - 1) / sub) * sub, jb = (T - 1) / sub;  // largest sub-block start <= the walk position
+        for (int cc = nchunk - 1; cc >= 0; cc--) {
+            // this chunk's copies are done when only the copies of later-issued chunks are outstanding
+            int later = 0;
+            for (int j = 1; j < nslot && cc - j >= 0; j++) later += loads_of(cc - j);
+            X_.wait_loads(later);
+            X_.lds_sync();
+            if (wv == 0) {
+                const uint32_t* slot = ring + (cc % nslot) * slot_words;
+                const int nwc = chunk_nwc(cc);
+                uint32_t vst = 0, vg = 0, vpar = 0;
+#pragma unroll
+                for (int pi = NPC - 1; pi >= 0; pi--) {
+                    const int ta = cc * CK + 2 * pi;
+                    if (ta >= T || hit) continue;
+                    const int pt = MM::PT(pi);
+                    const int qq = (st >> 8) & (Q - 1), ll = (st >> 2) & 63, bb = st >> (8 + QB), jo = st & 3;
+                    const int ca = jo >> 1, cb = jo & 1;
+                    const int P = MM::OFF(pi) + bb * MM::PBLK(pt);
+                    const int w0 = P >> 5;
+                    const uint32_t* wp = slot + ((gs * Q + qq) * 64 + ll) * nwc + w0;
+                    const uint32_t W0 = X_.uniform(wp[0]);
+                    const uint32_t W1 = X_.uniform(wp[1]);
+                    const uint64_t V = ((uint64_t)W0 << 32) | W1;
+                    auto bits = [&](int Pp, int nbit) -> int {  // nbit bits from push Pp on, first push highest
+                        return (int)((V >> (64 - (Pp - 32 * w0) - nbit)) & ((1u << nbit) - 1u));
+                    };
+                    int h = 0, e = 0, pa = 0, pb = 0;  // pa / pb: parity class of steps ta / ta + 1
+                    if (MD == 0) {
+                        e = bits(P + 2 + ca, 1);
+                        h = bits(P + e, 1);
+                    } else if (MD == 1) {
+                        const int PF = P + 2 + ca * 4;
+                        const int p = bits(PF + 2 + cb, 1);
+                        e = bits(PF + p, 1);
+                        h = bits(P + e, 1);
+                        pa = pb = p;
+                    } else if (!EQ) {
+                        if (pt == 1) {  // D4 phase B: three sequential-min bits -> winner (c, b) = 0xEDEC map
+                            const int PF = P + 4 + ca * 10;
+                            const int v3 = bits(PF + 4 + 3 * cb, 3);
+                            const int idx = (0xEDEC >> (2 * v3)) & 3;
+                            cstar = idx >> 1;
+                            const int bsel = idx & 1;
+                            e = bits(PF + idx, 1);
+                            h = bits(P + 2 * e + cstar, 1);
+                            pb = bsel ^ cstar;
+                            pa = bsel;
+                        } else {  // D4 phase A, with the class chosen by the phase B that follows it
+                            const int PF = P + 2 + ca * 6;
+                            const int bsel = bits(PF + 2 + 2 * cb + cstar, 1);
+                            e = bits(PF + bsel, 1);
+                            h = bits(P + e, 1);
+                            pb = bsel ^ cstar;
+                            pa = bsel;
+                        }
+                    } else {
+                        if (pt == 1) {  // EQ phase B
+                            const int PF = P + 4 + ca * 4;
+                            cstar = bits(PF + 2 + cb, 1);
+                            e = bits(PF + cstar, 1);
+                            h = bits(P + 2 * e + cstar, 1);
+                        } else {  // EQ phase A
+                            const int PF = P + 2 + ca * 2;
+                            e = bits(PF + cstar, 1);
+                            h = bits(P + e, 1);
+                        }
+                        pa = pb = cstar;
+                    }
+                    const int smid = GE::mid(bb, 2 * ca + e, qq, ll);  // state at step ta
+                    const int j1 = 2 * pi + 1, j0 = 2 * pi;
+                    vst = lane == j1 ? (uint32_t)st : lane == j0 ? (uint32_t)smid : vst;
+                    vg = (lane == j1 || lane == j0) ? (uint32_t)gs : vg;
+                    vpar = lane == j1 ? (uint32_t)pb : lane == j0 ? (uint32_t)pa : vpar;
+                    if (ta + 1 == midpos || ta == midpos) {
+                        if (lane == 0) a.mid_st[n] = ta + 1 == midpos ? st : smid;
+                        hit = true;
+                        continue;
+                    }
+                    if (ta == 0) continue;
+                    st = GE::start((h << (RB - 1)) | (e << (RB - 2)) | bb, qq, ll);  // state at step ta - 1
+                    if (ta == nbnd) {  // sub-block start: the path came from the slot the merge chose
+                        if (G > 1) gs = s_gsel[jb * S + st];
+                        nbnd -= sub;
+                        jb--;
+                    }
+                }
+                const int tpos = cc * CK + lane;
+                if (lane < CK && tpos < T) {
+                    s_st[tpos] = (uint16_t)vst;
+                    s_g[tpos] = (uint8_t)vg;
+                    s_par[tpos] = (uint8_t)vpar;
+                }
+                if (lane == 0) s_ctl[2] = hit ? 1 : 0;
+            }
+            X_.lds_sync();
+            if (s_ctl[2]) {
+                X_.wait_loads(0);
+                store_best();
+                return;  // first tail-biting pass: only the state before mid_t is needed
+            }
+            if (cc - nslot >= 0) issue(cc - nslot);
+        }
+    }
+
+    // ---- reconstruction and code (tcq_viterbi.cu:662-682) -------------------------------------------
+    store_best();
+    float* rn = a.rec + (size_t)n * a.ld;
+    for (int t = tid; t < T; t += nthr) {
+        const int stt = s_st[t], gg = s_g[t];
+        const int lb = mk.label(stt);
+        const bool hi = mix > 0 && ((t / mix) & 1);
+        const int Ut = hi ? U_hi : U;
+        const int gi = cand ? (int)s_gc[(t / sub) * G + gg] : gg;
+        const float gt = hi ? s_gain_hi[gi] : s_gain[gi];
+        const float* tt = (hi ? s_tab_hi : s_tab) + lb * Ut;
+        const float xt = s_x[t];
+        float bestd = kSent, val = 0.f;
+        int bu = 0;
+        for (int u = MD ? (int)s_par[t] : 0; u < Ut; u += MD ? 2 : 1) {
+            const float v = gt * tt[u];
+            const float d = xt - v;
+            const float dd = d * d;
+            if (dd < bestd) {
+                bestd = dd;
+                val = v;
+                bu = u;
+            }
+        }
+        const int tp = (t + a.rot) % a.ld;
+        rn[tp] = val;
+        if (a.code) a.code[(size_t)n * a.ld + tp] = (gi << 16) | (lb * Ut + bu);
+    }
+}
+
+#undef LTQ_CSP
+#undef LTQ_PUSH0
+
+
+// ---- host side: argument validation and dispatch, shared by the gfx950 entry point and the CPU emulation ----
+
+// The reference's validation (tcq_viterbi.cu:748-751, 762-763) plus this implementation's limits.
+inline int tcq_check(const TcqArgs& a)
+{
+    const int G = a.G, Gfull = a.Gfull, U = a.U, U_hi = a.U_hi, sub = a.sub, T = a.T, S = a.S, pp = a.pp, nl = a.nl;
+    if (G > kMaxG || Gfull > kMaxG || (!a.gcand && Gfull != G) || U > kMaxU || U_hi > kMaxU || sub <= 0 ||
+        T % sub != 0 || (sub & 1) || T / sub > kMaxSubs || T > kMaxT || sub > 32 || sub * G * nl * (pp ? 2 : 1) > 4096 ||
+        (pp && (S != 1024 || a.mix > 0 || (T & 1))) || (pp >= 2 && ((T & 3) || (sub & 3))) || pp > 3 || pp < 0 ||
+        (nl != 4 && nl != 8 && nl != 16 && nl != 32) || a.ld < T || (S != 1024 && nl != 4) || nl * U > 4 * kMaxU ||
+        nl * U_hi > 4 * kMaxU)
+        return -1;
+    if ((S != 1024 && S != 256) || (G != 1 && G != 2 && G != 3 && G != 4 && G != 8)) return -1;
+    if (T <= 0 || !a.bp || (pp && !a.pbits) || !a.best || !a.rec) return -1;
+    return 0;
+}
+
+// Calls f.template run<NU, RB, MD, NL>() for the instance serving a (RB = 3 when G = 8 at S = 1024, so that a
+// workgroup stays at 16 wavefronts), after checking that the packed decisions fit the caller's scratch.
+template <class F>
+int tcq_dispatch(const TcqArgs& a, const F& f)
+{
+    auto go = [&](auto nu, auto rb, auto md) -> int {
+        constexpr int NU = decltype(nu)::value, RB = decltype(rb)::value, MD = decltype(md)::value;
+        if (needed_words<NU, RB, MD>(a.T, a.G) > scratch_words(a.T, a.G, a.S, a.pp)) return -1;
+        switch (a.nl) {
+            case 4: return f.template run<NU, RB, MD, 4>();
+            case 8: return f.template run<NU, RB, MD, 8>();
+            case 16: return f.template run<NU, RB, MD, 16>();
+            default: return f.template run<NU, RB, MD, 32>();
+        }
+    };
+    using I8 = std::integral_constant<int, 8>;
+    using I10 = std::integral_constant<int, 10>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    if (a.S == 256) {
+        if (needed_words<8, 2, 0>(a.T, a.G) > scratch_words(a.T, a.G, a.S, a.pp)) return -1;
+        return f.template run<8, 2, 0, 4>();
+    }
+    const bool r3 = a.G > 4;
+    auto by_md = [&](auto rb) -> int {
+        switch (a.pp) {
+            case 0: return go(I10{}, rb, std::integral_constant<int, 0>{});
+            case 1: return go(I10{}, rb, std::integral_constant<int, 1>{});
+            case 2: return go(I10{}, rb, std::integral_constant<int, 2>{});
+            default: return go(I10{}, rb, std::integral_constant<int, 3>{});
+        }
+    };
+    (void)sizeof(I8);
+    return r3 ? by_md(I3{}) : by_md(I2{});
+}
+
+}  // namespace ltq

@@ -3,7 +3,8 @@
 // C ABI replaced: src/cuda/tcq_viterbi.cu:743-766 (tcq_viterbi) and :806-811 (lut_subs_quant); the argument
 // lists, buffer shapes and return codes are the reference's (0 = ok, -1 = rejected configuration, otherwise
 // the HIP error code of the launch). The caller allocates every buffer, as in the reference; bp / pbits are
-// used as opaque scratch for this kernel's own decision-word format, gsel is not touched.
+// used as opaque scratch for this kernel's own decision-word format, gsel is not touched. A configuration
+// whose packed decisions do not fit bp + pbits is rejected with -1.
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 
@@ -14,23 +15,14 @@
 namespace ltq {
 
 // instantiated in tcq_inst_*.hip (compiled in parallel)
-extern template int launch<8, 0, 4>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 0, 4>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 0, 8>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 0, 16>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 0, 32>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 1, 4>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 1, 8>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 1, 16>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 1, 32>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 2, 4>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 2, 8>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 2, 16>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 2, 32>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 3, 4>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 3, 8>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 3, 16>(const TcqArgs&, hipStream_t);
-extern template int launch<10, 3, 32>(const TcqArgs&, hipStream_t);
+#define LTQ_EXT(NU, RB, MD, NL) extern template int launch<NU, RB, MD, NL>(const TcqArgs&, hipStream_t);
+#define LTQ_EXT_MD(MD)                                                                                \
+    LTQ_EXT(10, 2, MD, 4) LTQ_EXT(10, 2, MD, 8) LTQ_EXT(10, 2, MD, 16) LTQ_EXT(10, 2, MD, 32)        \
+    LTQ_EXT(10, 3, MD, 4) LTQ_EXT(10, 3, MD, 8) LTQ_EXT(10, 3, MD, 16) LTQ_EXT(10, 3, MD, 32)
+LTQ_EXT(8, 2, 0, 4)
+LTQ_EXT_MD(0) LTQ_EXT_MD(1) LTQ_EXT_MD(2) LTQ_EXT_MD(3)
+#undef LTQ_EXT_MD
+#undef LTQ_EXT
 
 int device_lds_max()
 {
@@ -44,17 +36,15 @@ int device_lds_max()
     return v;
 }
 
-template <int NU, int MD>
-static int launch_nl(const TcqArgs& a, hipStream_t st)
-{
-    switch (a.nl) {
-        case 4: return launch<NU, MD, 4>(a, st);
-        case 8: return launch<NU, MD, 8>(a, st);
-        case 16: return launch<NU, MD, 16>(a, st);
-        case 32: return launch<NU, MD, 32>(a, st);
-        default: return -1;
+struct GpuLaunch {
+    const TcqArgs& a;
+    hipStream_t st;
+    template <int NU, int RB, int MD, int NL>
+    int run() const
+    {
+        return launch<NU, RB, MD, NL>(a, st);
     }
-}
+};
 
 }  // namespace ltq
 
@@ -67,29 +57,12 @@ extern "C" int tcq_viterbi(const float* x, const float* w, const float* tab, con
                            int ld, int rot, uint32_t* pbits, int pp, void* stream)
 {
     using namespace ltq;
-    // the reference's validation (tcq_viterbi.cu:748-751, 762-763)
-    if (G > kMaxG || Gfull > kMaxG || (!gcand && Gfull != G) || U > kMaxU || U_hi > kMaxU || sub <= 0 || T % sub != 0 ||
-        (sub & 1) || T / sub > kMaxSubs || T > kMaxT || sub > 32 || sub * G * nl * (pp ? 2 : 1) > 4096 ||
-        (pp && (S != 1024 || mix > 0 || (T & 1))) || (pp >= 2 && ((T & 3) || (sub & 3))) || pp > 3 || pp < 0 ||
-        (nl != 4 && nl != 8 && nl != 16 && nl != 32) || ld < T || ((S != 1024 || getenv("TCQ_BLOCK")) && nl != 4) ||
-        nl * U > 4 * kMaxU || nl * U_hi > 4 * kMaxU)
-        return -1;
-    if (S != 1024 && S != 256) return -1;
-    if (G != 1 && G != 2 && G != 3 && G != 4 && G != 8) return -1;
-    // limits of this implementation's decision-word storage inside the reference-sized scratch
-    if (pp == 1 && (T & 3)) return -1;
-    if (S == 256 && T < 8) return -1;
-    if (T <= 0 || !bp || (pp && !pbits) || !best || !rec) return -1;
-    if (N <= 0) return N == 0 ? (int)hipErrorInvalidConfiguration : -1;  // a 0-block launch, as the reference gets
     TcqArgs a{x, w, tab, gains, rec, bp, gsel, init_st, end_st, tab_hi, gains_hi, gcand, best, code, mid_st,
               mid_t, tail, N, T, S, U, G, Gfull, m, sub, U_hi, mix, m2, m3, m4, nl, ld, rot, pbits, pp};
-    hipStream_t st = (hipStream_t)stream;
-    int rc;
-    if (S == 256) rc = launch<8, 0, 4>(a, st);
-    else if (pp == 0) rc = launch_nl<10, 0>(a, st);
-    else if (pp == 1) rc = launch_nl<10, 1>(a, st);
-    else if (pp == 2) rc = launch_nl<10, 2>(a, st);
-    else rc = launch_nl<10, 3>(a, st);
+    // the reference also rejects any label count but 4 when TCQ_BLOCK is set (tcq_viterbi.cu:750)
+    if (tcq_check(a) != 0 || (getenv("TCQ_BLOCK") && nl != 4)) return -1;
+    if (N <= 0) return N == 0 ? (int)hipErrorInvalidConfiguration : -1;  // a 0-block launch, as the reference gets
+    const int rc = tcq_dispatch(a, GpuLaunch{a, (hipStream_t)stream});
     if (rc != 0) return rc;
     return (int)hipGetLastError();
 }

@@ -1,4 +1,4 @@
-"""The gfx950 kernel source (ltq-research_amd/csrc/tcq_kernel.h) compiled for the host and run with one
+"""The gfx950 kernel source (ltq-research_amd/csrc/tcq_trellis.h) compiled for the host and run with one
 thread per lane (tests/emu) must match the oracle bit for bit: pins the register layout, decision-word
 format and traceback indexing on the CPU, for every parity mode, before any GPU run."""
 import sys
@@ -24,6 +24,20 @@ CASES = [
     dict(pp=0, ext=(), G=2, T=36, sub=6),
     dict(pp=0, ext=(40, 475), G=2, T=64, mix=16),
     dict(pp=2, ext=(211, 397), G=1, T=32),
+    # 8 gain slots (8 states per lane, 2 wavefronts per slot), every mode
+    dict(pp=0, ext=(), G=8, T=48, init=True, tail=True),
+    dict(pp=1, ext=(241,), G=8, T=64),
+    dict(pp=2, ext=(241,), G=8, T=32, sub=8),
+    dict(pp=3, ext=(), G=8, T=32, U=8),
+    # partial last chunks, odd mid positions, more label counts, candidates in integer mode
+    dict(pp=0, ext=(), G=2, T=20, sub=10, mid_t=7),
+    dict(pp=1, ext=(), G=2, T=40, sub=8, mid_t=13, ld=48, rot=5),
+    dict(pp=1, ext=(241,), G=3, T=34, sub=2),
+    dict(pp=2, ext=(241,), G=4, T=20, sub=4, mid_t=10),
+    dict(pp=3, ext=(40,), G=2, T=36, sub=12, U=8, init=True, tail=True),
+    dict(pp=2, ext=(40, 475, 211), G=2, T=32),
+    dict(pp=0, ext=(40, 475, 211), G=4, T=32, n_cand=4, Gfull=8),
+    dict(pp=0, ext=(), G=1, T=64, S=256, mid_t=33),
 ]
 
 
