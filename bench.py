@@ -32,7 +32,9 @@ M_ROWS, K_COLS, N_OUTLIER, N_ACT = 4096, 14336, 143, 2048
 FORMAT = "TCQ275X2"
 TB_WINDOW = 32          # TCQ_TB_WIN default (src/liqk_v2.py:918)
 DAMP = 0.2              # 0.02 * TCQ_DAMP_MULT (src/liqk_v2.py:1061-1063)
-VALU_PEAK_TOPS = 78.6   # MI355X fp32 vector: 157.3 TFLOP/s counting an FMA as 2 -> 78.6e12 single-op lanes/s
+# gfx950 VALU: one non-packed wave64 instruction per 4 cycles per SIMD (measured: 3.1-3.5e13 lane-ops/s for
+# v_sub_f32 / v_alignbit_b32 at 1-4 waves per SIMD) = 256 CU x 4 SIMD x 16 lanes x 2.4 GHz
+VALU_PEAK_TOPS = 39.3
 LANE_OPS_PER_STEP = {0: 2.0, 1: 4.5, 2: 8.25, 3: 8.25}  # per state, per weight, per gain slot (radix-4 ACS)
 
 

@@ -1,7 +1,8 @@
 """Builds libltq_hip.so for gfx950 in-tree (ltq_amd/libltq_hip.so) from csrc/*.hip.
 
 Flags: -ffp-contract=off (no FMA contraction: the quantizer's fp32 arithmetic must match the reference's
-torch order of operations bit for bit) and packed-fp32 instructions disabled."""
+torch order of operations bit for bit), packed-fp32 instructions disabled, and -fno-honor-nans for the
+Viterbi units (see EXTRA)."""
 from __future__ import annotations
 
 import os
@@ -19,6 +20,16 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=o
          "-I", str(HERE.parent / "include")]
 
 
+# the Viterbi kernels compare and add path metrics that are never NaN or -0 (sums of squared errors >= +0
+# under a 3.4e38 sentinel): without NaN semantics the compiler keeps v_min_f32 operands as they are instead of
+# canonicalizing each one first, with bit-identical results
+EXTRA = {"tcq_inst_": ["-fno-honor-nans"]}
+
+
+def _extra(name: str):
+    return [f for k, v in EXTRA.items() if name.startswith(k) for f in v]
+
+
 def build(verbose: bool = False) -> Path:
     srcs = sorted(CSRC.glob("*.hip"))
     objdir = HERE / "_build"
@@ -26,7 +37,7 @@ def build(verbose: bool = False) -> Path:
 
     def compile_one(src: Path) -> Path:
         obj = objdir / (src.stem + ".o")
-        cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *FLAGS, *_extra(src.name), "-c", str(src), "-o", str(obj)]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stderr}")

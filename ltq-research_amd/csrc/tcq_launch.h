@@ -34,10 +34,10 @@ struct GpuX {
     __device__ __forceinline__ float fmin(float x, float y) const { return __builtin_fminf(x, y); }
     __device__ __forceinline__ float shfl_xor(float v, int m) const { return __shfl_xor(v, m, 64); }
     __device__ __forceinline__ int shfl_xor(int v, int m) const { return __shfl_xor(v, m, 64); }
-    // a value every lane of the wave holds: kept in a scalar register
-    __device__ __forceinline__ uint32_t uniform(uint32_t v) const
+    // lane l's value (l uniform), into a scalar register
+    __device__ __forceinline__ uint32_t readlane(uint32_t v, int l) const
     {
-        return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+        return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
     }
     // asynchronous 16-byte copy global -> LDS; lane l's bytes land at lds_wave_base + 16 l
     __device__ __forceinline__ void load16(const uint32_t* src, uint32_t* lds_wave_base) const

@@ -119,6 +119,16 @@ struct Md {
 
 LTQ_HD int align16(int v) { return (v + 15) & ~15; }
 
+// f(integral_constant<I>), ..., f(integral_constant<N-1>): a loop whose index is a compile-time constant
+template <int I, int N, class F>
+LTQ_DEV void static_for(F&& f)
+{
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
 struct alignas(16) F4 {
     float x, y, z, w;
 };
@@ -164,7 +174,7 @@ LTQ_HD Smem smem_layout(int T, int G, int Gfull, int sub, int lds_max)
     const int fwd_end = L.dbl ? two : one;
     // ring slots: one chunk of decision words of every (gain slot, wave, lane), whole 1 KB wave loads + pad
     const int cw = G * GE::Q * 64 * MM::NW;
-    L.slot_words = ((cw + 255) / 256) * 256 + 256;
+    L.slot_words = ((cw + 255) / 256) * 256 + 256;  // + pad: the walker reads word w + 1 of any lane
     L.ring = L.tabs;
     int ns = 4;
     while (ns > 2 && L.ring + ns * 4 * L.slot_words > lds_max && L.ring + ns * 4 * L.slot_words > fwd_end) ns--;
@@ -202,7 +212,7 @@ LTQ_DEV float level_err(float xt, float gain, const float* tb, int u0, int Ut, i
         const float v = gain * tb[u];
         const float d = xt - v;
         const float dd = d * d;
-        e = dd < e ? dd : e;
+        e = dd < e ? dd : e;  // v_min_f32: dd and e are never NaN
     }
     return e;
 }
@@ -226,8 +236,8 @@ LTQ_DEV float level_err(float xt, float gain, const float* tb, int u0, int Ut, i
 // high state bit wins only when strictly smaller (p0 on ties), as in the reference.
 // ma[jj][p]: metric of intermediate jj (step a), mb[j][p]: metric of output j (step b), p = parity class.
 // ------------------------------------------------------------------------------------------------
-template <int MD, int PT, int P0, class X>
-LTQ_DEV void run_block(bool init, const bool (&ok)[4], const float (&I)[2][4], const float (&ma)[4][2],
+template <int MD, int PT, int P0, bool init, class X>
+LTQ_DEV void run_block(const bool (&ok)[4], const float (&I)[2][4], const float (&ma)[4][2],
                        const float (&mb)[4][2], float (&O)[2][4], uint32_t* acc, X& X_)
 {
     constexpr bool EQ = MD == 3;
@@ -236,7 +246,7 @@ LTQ_DEV void run_block(bool init, const bool (&ok)[4], const float (&I)[2][4], c
 #pragma unroll
         for (int e = 0; e < 2; e++) {
             const int j0 = e, j1 = 2 + e;
-            if (init) {
+            if constexpr (init) {
                 v[j0] = ok[j0] ? ma[j0][0] : kSent;
                 v[j1] = ok[j1] ? ma[j1][0] : kSent;
                 LTQ_PUSH0(P0 + e);
@@ -261,7 +271,7 @@ LTQ_DEV void run_block(bool init, const bool (&ok)[4], const float (&I)[2][4], c
 #pragma unroll
         for (int e = 0; e < 2; e++) {
             const int j0 = e, j1 = 2 + e;
-            if (init) {
+            if constexpr (init) {
 #pragma unroll
                 for (int qq = 0; qq < 2; qq++) {
                     const int jj = qq ? j1 : j0;
@@ -392,7 +402,7 @@ struct DecMap {
 // The per-tile kernel body.
 // X provides: tid(), wave() (tid / 64, uniform), tile(), nthreads(), smem(), sync() (full barrier incl. global
 // memory), lds_sync() (barrier for LDS only), push_sign(acc, d), fmin(x, y), shfl_xor(v, mask) (within a
-// wavefront), uniform(v) (value of lane 0), load16(global src, LDS wave base) (asynchronous 16-byte
+// wavefront), readlane(v, l) (lane l's value, l uniform), load16(global src, LDS wave base) (asynchronous 16-byte
 // global -> LDS copy landing at base + 16 * lane), wait_loads(n) (at most n such copies of this wave still
 // outstanding, n <= 15).
 // ------------------------------------------------------------------------------------------------
@@ -542,76 +552,67 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
     float O[2][NB][4];
     uint32_t acc[NW];
 
+    // metrics of in-chunk phase PI (steps 2 PI, 2 PI + 1 of the chunk) for every (block, slot)
+    float ma[NB][4][2], mb[NB][4][2];
+    auto load_metrics = [&](const float* tb, auto PIc) {
+        constexpr int pi = decltype(PIc)::value;
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int p = 0; p < NP; p++) {
+                    ma[b][j][p] = tb[offa[b][j] + (2 * pi) * NL * NP + p];
+                    mb[b][j][p] = tb[offb[b][j] + (2 * pi + 1) * NL * NP + p];
+                }
+    };
+
     tables(0);
     X_.lds_sync();
+    load_metrics(s_tabs, std::integral_constant<int, 0>{});
     int xph = 0;                         // global phase counter (exchange buffer parity)
     int next_merge = sub, merge_j = 1;   // next sub-block boundary and its index
-    for (int c = 0; c < nchunk; c++) {
+    // chunk c; FIRST: chunk 0, whose phase 0 starts the trellis (compile-time, so no other phase carries the
+    // start-state selects)
+    auto chunk = [&](int c, auto FIRSTc) {
+        constexpr bool FIRST = decltype(FIRSTc)::value;
 #pragma unroll
         for (int w = 0; w < NW; w++) acc[w] = 0;
         const float* tb = s_tabs + (c & 1) * TF;
+        const float* tbn = s_tabs + ((c + 1) & 1) * TF;
         int real = 0;  // phases of this chunk inside the tile
-#pragma unroll
-        for (int pi = 0; pi < NPC; pi++) {
+        static_for<0, NPC>([&](auto PIc) {
+            constexpr int pi = decltype(PIc)::value;
+            constexpr int PT = MM::PT(pi);
             const int ta = c * CK + 2 * pi;
             if (ta >= T) {  // beyond the tile end: zero pushes keep every decision bit at its fixed position
 #pragma unroll
-                for (int i = 0; i < MM::PPH(MM::PT(pi)); i++) LTQ_PUSH0(MM::OFF(pi) + i);
-                continue;
+                for (int i = 0; i < MM::PPH(PT); i++) LTQ_PUSH0(MM::OFF(pi) + i);
+                return;
             }
             real++;
-            // metrics of steps ta, ta + 1 for every (block, slot)
-            float ma[NB][4][2], mb[NB][4][2];
+            constexpr bool init = FIRST && pi == 0;
+            static_for<0, NB>([&](auto Bc) {
+                constexpr int b = decltype(Bc)::value;
+                float Ib[2][4], Ob[2][4];
 #pragma unroll
-            for (int b = 0; b < NB; b++)
+                for (int cc2 = 0; cc2 < 2; cc2++)
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+                    for (int j = 0; j < 4; j++) Ib[cc2][j] = I[cc2][b][j];
+                run_block<MD, PT, MM::OFF(pi) + b * MM::PBLK(PT), init>(ok[b], Ib, ma[b], mb[b], Ob, acc, X_);
 #pragma unroll
-                    for (int p = 0; p < NP; p++) {
-                        ma[b][j][p] = tb[offa[b][j] + (2 * pi) * NL * NP + p];
-                        mb[b][j][p] = tb[offb[b][j] + (2 * pi + 1) * NL * NP + p];
-                    }
-            const bool init = ta == 0;
-            // run the blocks (compile-time phase type and push offsets)
-#define LTQ_RUN_PHASE(PTv, PIv)                                                                            \
-    do {                                                                                                   \
-        _Pragma("unroll") for (int b = 0; b < NB; b++)                                                     \
-        {                                                                                                  \
-            float Ib[2][4], Ob[2][4];                                                                      \
-            _Pragma("unroll") for (int cc2 = 0; cc2 < 2; cc2++)                                            \
-                _Pragma("unroll") for (int j = 0; j < 4; j++) Ib[cc2][j] = I[cc2][b][j];                   \
-            if (b == 0)                                                                                    \
-                run_block<MD, PTv, MM::OFF(PIv) + 0 * MM::PBLK(PTv)>(init, ok[0], Ib, ma[0], mb[0], Ob, acc, X_); \
-            else                                                                                           \
-                run_block<MD, PTv, MM::OFF(PIv) + 1 * MM::PBLK(PTv)>(init, ok[NB - 1], Ib, ma[NB - 1],     \
-                                                                    mb[NB - 1], Ob, acc, X_);              \
-            _Pragma("unroll") for (int cc2 = 0; cc2 < 2; cc2++)                                            \
-                _Pragma("unroll") for (int j = 0; j < 4; j++) O[cc2][b][j] = Ob[cc2][j];                   \
-        }                                                                                                  \
-    } while (0)
-            switch (pi) {
-                case 0: LTQ_RUN_PHASE(MM::PT(0), 0); break;
-                case 1: LTQ_RUN_PHASE(MM::PT(1), 1); break;
-                case 2: LTQ_RUN_PHASE(MM::PT(2), 2); break;
-                case 3: LTQ_RUN_PHASE(MM::PT(3), 3); break;
-                case 4: LTQ_RUN_PHASE(MM::PT(4), 4); break;
-                case 5: LTQ_RUN_PHASE(MM::PT(5), 5); break;
-                case 6: LTQ_RUN_PHASE(MM::PT(6), 6); break;
-                case 7: LTQ_RUN_PHASE(MM::PT(7), 7); break;
-                case 8: LTQ_RUN_PHASE(MM::PT(8 % NPC), 8 % NPC); break;
-                case 9: LTQ_RUN_PHASE(MM::PT(9 % NPC), 9 % NPC); break;
-                case 10: LTQ_RUN_PHASE(MM::PT(10 % NPC), 10 % NPC); break;
-                case 11: LTQ_RUN_PHASE(MM::PT(11 % NPC), 11 % NPC); break;
-                case 12: LTQ_RUN_PHASE(MM::PT(12 % NPC), 12 % NPC); break;
-                case 13: LTQ_RUN_PHASE(MM::PT(13 % NPC), 13 % NPC); break;
-                case 14: LTQ_RUN_PHASE(MM::PT(14 % NPC), 14 % NPC); break;
-                default: LTQ_RUN_PHASE(MM::PT(15 % NPC), 15 % NPC); break;
-            }
-#undef LTQ_RUN_PHASE
+                for (int cc2 = 0; cc2 < 2; cc2++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) O[cc2][b][j] = Ob[cc2][j];
+            });
             const int tn = ta + 2;
-            if (tn >= T) continue;  // last phase: outputs stay in registers for the argmin
+            if (tn >= T) return;  // last phase: outputs stay in registers for the argmin
+            // next phase's metrics: the tables were written before an earlier barrier, so the loads can fly
+            // while this wave waits at the exchange barrier
+            if constexpr (pi + 1 < NPC) load_metrics(tb, std::integral_constant<int, pi + 1>{});
+            else load_metrics(tbn, std::integral_constant<int, 0>{});
             // ---- exchange into the next phase's start layout (+ gain merge at a sub-block boundary) ----
-            const bool carry2 = TWO && MM::PT(pi) == 0;  // phase A -> B carries two class planes
+            constexpr bool carry2 = TWO && PT == 0;  // phase A -> B carries two class planes
             float* xb = s_exch + (SM.dbl ? (xph & 1) : 0) * SM.exch_floats;
             if (!SM.dbl) X_.lds_sync();  // single buffer: every wave has read the previous exchange
 #pragma unroll
@@ -634,21 +635,26 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
                 next_merge += sub;
                 merge_j++;
             }
-            if (G > 1 && at_sub) {
+            if (!carry2 && G > 1 && at_sub) {
+                // gain merge: per state the lowest metric over the slots, lowest slot on ties (slots >= G read
+                // slot 0's value again, which never wins the strict compare)
 #pragma unroll
                 for (int b = 0; b < NB; b++)
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         const int s = GE::start((j << (RB - 2)) | b, q, lane);
-                        float bv = xb[s];
+                        constexpr int GM = 16 / Q < 8 ? 16 / Q : 8;  // most gain slots this geometry serves
+                        float v[GM];
+#pragma unroll
+                        for (int gg = 0; gg < GM; gg++) v[gg] = xb[(gg < G ? gg : 0) * XF * S + s];
+                        float bv = v[0];
                         int bg = 0;
-                        for (int gg = 1; gg < G; gg++) {
-                            const float v = xb[gg * XF * S + s];
-                            if (v < bv) {
-                                bv = v;
+#pragma unroll
+                        for (int gg = 1; gg < GM; gg++)
+                            if (v[gg] < bv) {
+                                bv = v[gg];
                                 bg = gg;
                             }
-                        }
                         I[0][b][j] = bv;
                         if (g == 0) s_gsel[jm * S + s] = (uint8_t)bg;
                     }
@@ -661,16 +667,19 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
                         for (int j = 0; j < 4; j++)  // slot j of block b is register (j << (RB - 2)) | b
                             I[cp][b][j] = xb[(g * XF + cp) * S + GE::start((j << (RB - 2)) | b, q, lane)];
             }
-        }
+        });
         // ---- store this chunk's decision words (left-aligned), only the words holding real bits -------
         if (MM::LAST < 32) acc[NW - 1] <<= (32 - MM::LAST) & 31;
         const int rbits = TWO ? (real / 2) * (MM::PPH(0) + MM::PPH(1)) + (real & 1) * MM::PPH(0) : real * MM::PPH(0);
         const int nwc = real == NPC ? NW : (rbits + 31) / 32;
-        const long L0 = (long)c * chunk_words + ((long)(g * Q + q) * 64 + lane) * nwc;
+        // word-major: word w of every lane of (slot g, wave q) is 64 consecutive u32 (coalesced stores)
+        const long L0 = (long)c * chunk_words + (long)(g * Q + q) * nwc * 64 + lane;
 #pragma unroll
         for (int w = 0; w < NW; w++)
-            if (w < nwc) *dm.at(L0 + w) = acc[w];
-    }
+            if (w < nwc) *dm.at(L0 + 64L * w) = acc[w];
+    };
+    chunk(0, std::true_type{});
+    for (int c = 1; c < nchunk; c++) chunk(c, std::false_type{});
 
     // ---- argmin over (g, s), lowest index on ties (tcq_viterbi.cu:561-578) ---------------------------
     {
@@ -717,7 +726,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
         }
         X_.lds_sync();
     }
-    const int bi_all = s_ctl[0];
+    const int bi_all = (int)X_.readlane((uint32_t)s_ctl[0], 0);  // uniform: scalar registers
     // best / end state are stored after the traceback's copies are drained (no global store may sit among the
     // copies a wave counts with wait_loads)
     auto store_best = [&]() {
@@ -767,6 +776,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
         bool hit = false;
         const int midpos = a.mid_st ? a.mid_t - 1 : -1;
         int nbnd = ((T - 1) / sub) * sub, jb = (T - 1) / sub;  // largest sub-block start <= the walk position
+        uint32_t* s_rec = (uint32_t*)s_st;  // per phase: (state | slot << 10 | class << 15) of its two steps
         for (int cc = nchunk - 1; cc >= 0; cc--) {
             // this chunk's copies are done when only the copies of later-issued chunks are outstanding
             int later = 0;
@@ -776,35 +786,58 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
             if (wv == 0) {
                 const uint32_t* slot = ring + (cc % nslot) * slot_words;
                 const int nwc = chunk_nwc(cc);
-                uint32_t vst = 0, vg = 0, vpar = 0;
-#pragma unroll
-                for (int pi = NPC - 1; pi >= 0; pi--) {
+                // word index of the first decision word of phase PI for output state sx
+                auto word_at = [&](int sx, int PI) -> int {
+                    const int P = MM::OFF(PI) + (sx >> (8 + QB)) * MM::PBLK(MM::PT(PI));
+                    return ((gs * Q + ((sx >> 8) & (Q - 1))) * nwc + (P >> 5)) * 64 + ((sx >> 2) & 63);
+                };
+                // candidate words: lane i holds the two words of hypothesis i (the input slot bits h e = i of
+                // the phase walked before) -- loaded one phase ahead; sel picks the true one
+                uint32_t c0 = 0, c1 = 0;
+                int sel = 0;
+                bool need = true;  // candidates not loaded (chunk start, or the gain slot changed)
+                uint32_t vrec = 0;
+                static_for<0, NPC>([&](auto Kc) {
+                    constexpr int pi = NPC - 1 - decltype(Kc)::value;
+                    constexpr int PT = MM::PT(pi);
                     const int ta = cc * CK + 2 * pi;
-                    if (ta >= T || hit) continue;
-                    const int pt = MM::PT(pi);
+                    if (ta >= T || hit) return;
+                    if (need) {  // exact words of this phase into every lane
+                        const int wi = word_at(st, pi);
+                        c0 = slot[wi];
+                        c1 = slot[wi + 64];
+                        sel = 0;
+                        need = false;
+                    }
+                    const uint32_t W0 = X_.readlane(c0, sel), W1 = X_.readlane(c1, sel);
                     const int qq = (st >> 8) & (Q - 1), ll = (st >> 2) & 63, bb = st >> (8 + QB), jo = st & 3;
+                    // prefetch the next phase's candidates (this chunk only; a new chunk starts exact)
+                    if (pi > 0 && ta > 0) {
+                        const int hyp = lane & 3;
+                        const int sx = GE::start((hyp << (RB - 2)) | bb, qq, ll);
+                        const int wi = word_at(sx, pi > 0 ? pi - 1 : 0);
+                        c0 = slot[wi];
+                        c1 = slot[wi + 64];
+                    }
                     const int ca = jo >> 1, cb = jo & 1;
-                    const int P = MM::OFF(pi) + bb * MM::PBLK(pt);
+                    const int P = MM::OFF(pi) + bb * MM::PBLK(PT);
                     const int w0 = P >> 5;
-                    const uint32_t* wp = slot + ((gs * Q + qq) * 64 + ll) * nwc + w0;
-                    const uint32_t W0 = X_.uniform(wp[0]);
-                    const uint32_t W1 = X_.uniform(wp[1]);
                     const uint64_t V = ((uint64_t)W0 << 32) | W1;
                     auto bits = [&](int Pp, int nbit) -> int {  // nbit bits from push Pp on, first push highest
                         return (int)((V >> (64 - (Pp - 32 * w0) - nbit)) & ((1u << nbit) - 1u));
                     };
                     int h = 0, e = 0, pa = 0, pb = 0;  // pa / pb: parity class of steps ta / ta + 1
-                    if (MD == 0) {
+                    if constexpr (MD == 0) {
                         e = bits(P + 2 + ca, 1);
                         h = bits(P + e, 1);
-                    } else if (MD == 1) {
+                    } else if constexpr (MD == 1) {
                         const int PF = P + 2 + ca * 4;
                         const int p = bits(PF + 2 + cb, 1);
                         e = bits(PF + p, 1);
                         h = bits(P + e, 1);
                         pa = pb = p;
-                    } else if (!EQ) {
-                        if (pt == 1) {  // D4 phase B: three sequential-min bits -> winner (c, b) = 0xEDEC map
+                    } else if constexpr (!EQ) {
+                        if constexpr (PT == 1) {  // D4 phase B: three sequential-min bits -> winner (c, b) = 0xEDEC map
                             const int PF = P + 4 + ca * 10;
                             const int v3 = bits(PF + 4 + 3 * cb, 3);
                             const int idx = (0xEDEC >> (2 * v3)) & 3;
@@ -823,7 +856,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
                             pa = bsel;
                         }
                     } else {
-                        if (pt == 1) {  // EQ phase B
+                        if constexpr (PT == 1) {  // EQ phase B
                             const int PF = P + 4 + ca * 4;
                             cstar = bits(PF + 2 + cb, 1);
                             e = bits(PF + cstar, 1);
@@ -836,29 +869,29 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
                         pa = pb = cstar;
                     }
                     const int smid = GE::mid(bb, 2 * ca + e, qq, ll);  // state at step ta
-                    const int j1 = 2 * pi + 1, j0 = 2 * pi;
-                    vst = lane == j1 ? (uint32_t)st : lane == j0 ? (uint32_t)smid : vst;
-                    vg = (lane == j1 || lane == j0) ? (uint32_t)gs : vg;
-                    vpar = lane == j1 ? (uint32_t)pb : lane == j0 ? (uint32_t)pa : vpar;
+                    const uint32_t rec2 = (uint32_t)(smid | (gs << 10) | (pa << 15)) |
+                                          ((uint32_t)(st | (gs << 10) | (pb << 15)) << 16);
+                    vrec = lane == pi ? rec2 : vrec;
                     if (ta + 1 == midpos || ta == midpos) {
                         if (lane == 0) a.mid_st[n] = ta + 1 == midpos ? st : smid;
                         hit = true;
-                        continue;
+                        return;
                     }
-                    if (ta == 0) continue;
+                    if (ta == 0) return;
+                    sel = 2 * h + e;
                     st = GE::start((h << (RB - 1)) | (e << (RB - 2)) | bb, qq, ll);  // state at step ta - 1
                     if (ta == nbnd) {  // sub-block start: the path came from the slot the merge chose
-                        if (G > 1) gs = s_gsel[jb * S + st];
+                        if (G > 1) {
+                            const int gn = (int)X_.readlane(s_gsel[jb * S + st], 0);
+                            need = gn != gs;
+                            gs = gn;
+                        }
                         nbnd -= sub;
                         jb--;
                     }
-                }
-                const int tpos = cc * CK + lane;
-                if (lane < CK && tpos < T) {
-                    s_st[tpos] = (uint16_t)vst;
-                    s_g[tpos] = (uint8_t)vg;
-                    s_par[tpos] = (uint8_t)vpar;
-                }
+                });
+                const int rp = cc * NPC + lane;
+                if (lane < NPC && 2 * rp < T) s_rec[rp] = vrec;
                 if (lane == 0) s_ctl[2] = hit ? 1 : 0;
             }
             X_.lds_sync();
@@ -874,8 +907,10 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
     // ---- reconstruction and code (tcq_viterbi.cu:662-682) -------------------------------------------
     store_best();
     float* rn = a.rec + (size_t)n * a.ld;
+    const uint32_t* s_rec = (const uint32_t*)s_st;
     for (int t = tid; t < T; t += nthr) {
-        const int stt = s_st[t], gg = s_g[t];
+        const uint32_t rr = s_rec[t >> 1] >> ((t & 1) * 16);
+        const int stt = rr & 1023, gg = (rr >> 10) & 15, par = (rr >> 15) & 1;
         const int lb = mk.label(stt);
         const bool hi = mix > 0 && ((t / mix) & 1);
         const int Ut = hi ? U_hi : U;
@@ -885,7 +920,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
         const float xt = s_x[t];
         float bestd = kSent, val = 0.f;
         int bu = 0;
-        for (int u = MD ? (int)s_par[t] : 0; u < Ut; u += MD ? 2 : 1) {
+        for (int u = MD ? par : 0; u < Ut; u += MD ? 2 : 1) {
             const float v = gt * tt[u];
             const float d = xt - v;
             const float dd = d * d;
