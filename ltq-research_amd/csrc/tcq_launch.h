@@ -45,15 +45,17 @@ struct GpuX {
         __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)lds_wave_base,
                                          16, 0, 0);
     }
-    // at most n (<= 15) of this wave's vector memory operations still outstanding
+    // at most n (<= 63) of this wave's vector memory operations still outstanding (vmcnt: bits 3:0, 15:14)
     __device__ __forceinline__ void wait_loads(int n) const
     {
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         switch (n) {
 #define LTQ_W(k) \
-    case k: __builtin_amdgcn_s_waitcnt(k | 0xF70); break;
-            LTQ_W(1) LTQ_W(2) LTQ_W(3) LTQ_W(4) LTQ_W(5) LTQ_W(6) LTQ_W(7) LTQ_W(8) LTQ_W(9) LTQ_W(10) LTQ_W(11)
-            LTQ_W(12) LTQ_W(13) LTQ_W(14) LTQ_W(15)
+    case k: __builtin_amdgcn_s_waitcnt(((k) & 15) | (((k) >> 4) << 14) | 0xF70); break;
+#define LTQ_W8(k) LTQ_W(k) LTQ_W(k + 1) LTQ_W(k + 2) LTQ_W(k + 3) LTQ_W(k + 4) LTQ_W(k + 5) LTQ_W(k + 6) LTQ_W(k + 7)
+            LTQ_W(1) LTQ_W(2) LTQ_W(3) LTQ_W(4) LTQ_W(5) LTQ_W(6) LTQ_W(7)
+            LTQ_W8(8) LTQ_W8(16) LTQ_W8(24) LTQ_W8(32) LTQ_W8(40) LTQ_W8(48) LTQ_W8(56)
+#undef LTQ_W8
 #undef LTQ_W
             default: __builtin_amdgcn_s_waitcnt(0xF70); break;  // vmcnt(0)
         }

@@ -176,8 +176,12 @@ LTQ_HD Smem smem_layout(int T, int G, int Gfull, int sub, int lds_max)
     const int cw = G * GE::Q * 64 * MM::NW;
     L.slot_words = ((cw + 255) / 256) * 256 + 256;  // + pad: the walker reads word w + 1 of any lane
     L.ring = L.tabs;
+    // wavefront 0 keeps nslot - 1 chunks of copies in flight: at most 63 outstanding (vmcnt)
+    const int nl = (cw / 4 + 63) / 64;
     int ns = 4;
-    while (ns > 2 && L.ring + ns * 4 * L.slot_words > lds_max && L.ring + ns * 4 * L.slot_words > fwd_end) ns--;
+    while (ns > 2 && ((L.ring + ns * 4 * L.slot_words > lds_max && L.ring + ns * 4 * L.slot_words > fwd_end) ||
+                      (ns - 1) * nl > 63))
+        ns--;
     L.nslot = ns;
     const int ring_end = L.ring + ns * 4 * L.slot_words;
     L.total = fwd_end > ring_end ? fwd_end : ring_end;
@@ -404,7 +408,7 @@ struct DecMap {
 // memory), lds_sync() (barrier for LDS only), push_sign(acc, d), fmin(x, y), shfl_xor(v, mask) (within a
 // wavefront), readlane(v, l) (lane l's value, l uniform), load16(global src, LDS wave base) (asynchronous 16-byte
 // global -> LDS copy landing at base + 16 * lane), wait_loads(n) (at most n such copies of this wave still
-// outstanding, n <= 15).
+// outstanding, n <= 63).
 // ------------------------------------------------------------------------------------------------
 template <int NU, int RB, int MD, int NL, class X>
 LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
@@ -727,190 +731,167 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
         X_.lds_sync();
     }
     const int bi_all = (int)X_.readlane((uint32_t)s_ctl[0], 0);  // uniform: scalar registers
-    // best / end state are stored after the traceback's copies are drained (no global store may sit among the
-    // copies a wave counts with wait_loads)
-    auto store_best = [&]() {
-        if (tid == 0) {
-            a.best[n] = bi_all;
-            if (a.end_st) a.end_st[n] = bi_all % S;
-        }
-    };
+    // The traceback and the reconstruction run on wavefront 0 alone: the other wavefronts are done (no
+    // barrier follows), and wavefront 0 issues every decision-word copy itself, so that its own vmcnt
+    // tracks them.
+    if (wv != 0) return;
 
     // ---- traceback (tcq_viterbi.cu:601-661) ----------------------------------------------------------
     // One LDS lookup per phase: the phase's output state names the (wave, lane) that computed it and the
     // block; that lane's decision bits give the phase's input state, the intermediate state and the parity
-    // classes. Chunks of decision words are copied global -> LDS nslot chunks ahead by every wavefront.
+    // classes. Lanes 0-3 fetch the four possible next lookups one phase ahead; v_readlane picks the true one.
+    uint32_t* s_rec = (uint32_t*)s_st;  // per phase: output state | slot << 10 | e << 14 | classes << 15
     {
         uint32_t* ring = (uint32_t*)(sm + SM.ring);
         const int nslot = SM.nslot, slot_words = SM.slot_words;
-        const int nwaves = nthr / 64;
         const uint32_t* dummy = dm.bp;
         auto chunk_nwc = [&](int cc) {
             const int rp = (cc + 1) * NPC <= nph ? NPC : nph - cc * NPC;
             const int rb = TWO ? (rp / 2) * (MM::PPH(0) + MM::PPH(1)) + (rp & 1) * MM::PPH(0) : rp * MM::PPH(0);
             return rp == NPC ? NW : (rb + 31) / 32;
         };
-        // loads of one chunk: 16-byte units u = i * 64 + lane for wave loads i = wv, wv + nwaves, ...
-        const int lpw_max = ((G * Q * 16 * NW + 63) / 64 + nwaves - 1) / nwaves;
+        // copies of one chunk: 16-byte units u = i * 64 + lane for wave loads i = 0 .. nl-1
+        auto nloads = [&](int cc) { return (G * Q * 16 * chunk_nwc(cc) + 63) / 64; };
         auto issue = [&](int cc) {
-            const int units = G * Q * 16 * chunk_nwc(cc);
+            const int units = G * Q * 16 * chunk_nwc(cc), nl = (units + 63) / 64;
             uint32_t* slot = ring + (cc % nslot) * slot_words;
             const long base = (long)cc * chunk_words;
-            for (int k = 0; k < lpw_max; k++) {
-                const int i = wv + k * nwaves;
+            for (int i = 0; i < nl; i++) {
                 const int u = i * 64 + lane;
-                const uint32_t* src = u < units ? dm.at(base + 4L * u) : dummy;
-                if (i * 64 < units) X_.load16(src, slot + i * 256);
+                X_.load16(u < units ? dm.at(base + 4L * u) : dummy, slot + i * 256);
             }
-        };
-        auto loads_of = [&](int cc) {  // wave loads this wave issues for chunk cc
-            const int units = G * Q * 16 * chunk_nwc(cc);
-            int k = 0;
-            for (int kk = 0; kk < lpw_max; kk++)
-                if ((wv + kk * nwaves) * 64 < units) k++;
-            return k;
         };
         for (int j = 0; j < nslot; j++)
             if (nchunk - 1 - j >= 0) issue(nchunk - 1 - j);
         int st = bi_all % S, gs = bi_all / S, cstar = 0;
-        bool hit = false;
-        const int midpos = a.mid_st ? a.mid_t - 1 : -1;
+        const int mid_ph = a.mid_st ? (a.mid_t - 1) >> 1 : -1;  // phase holding the step before mid_t
         int nbnd = ((T - 1) / sub) * sub, jb = (T - 1) / sub;  // largest sub-block start <= the walk position
-        uint32_t* s_rec = (uint32_t*)s_st;  // per phase: (state | slot << 10 | class << 15) of its two steps
-        for (int cc = nchunk - 1; cc >= 0; cc--) {
+        bool done = false;
+        for (int cc = nchunk - 1; cc >= 0 && !done; cc--) {
             // this chunk's copies are done when only the copies of later-issued chunks are outstanding
             int later = 0;
-            for (int j = 1; j < nslot && cc - j >= 0; j++) later += loads_of(cc - j);
+            for (int j = 1; j < nslot && cc - j >= 0; j++) later += nloads(cc - j);
             X_.wait_loads(later);
-            X_.lds_sync();
-            if (wv == 0) {
-                const uint32_t* slot = ring + (cc % nslot) * slot_words;
-                const int nwc = chunk_nwc(cc);
-                // word index of the first decision word of phase PI for output state sx
-                auto word_at = [&](int sx, int PI) -> int {
-                    const int P = MM::OFF(PI) + (sx >> (8 + QB)) * MM::PBLK(MM::PT(PI));
-                    return ((gs * Q + ((sx >> 8) & (Q - 1))) * nwc + (P >> 5)) * 64 + ((sx >> 2) & 63);
+            const uint32_t* slot = ring + (cc % nslot) * slot_words;
+            const int nwc = chunk_nwc(cc);
+            // word index of the first decision word of phase PI for output state sx
+            auto word_at = [&](int sx, int PI) -> int {
+                const int P = MM::OFF(PI) + (sx >> (8 + QB)) * MM::PBLK(MM::PT(PI));
+                return ((gs * Q + ((sx >> 8) & (Q - 1))) * nwc + (P >> 5)) * 64 + ((sx >> 2) & 63);
+            };
+            uint32_t c0 = 0, c1 = 0;  // lane i: the two words of hypothesis i for the phase about to be walked
+            int sel = 0;
+            bool need = true;  // candidates not loaded (chunk start, or the gain slot changed)
+            static_for<0, NPC>([&](auto Kc) {
+                constexpr int pi = NPC - 1 - decltype(Kc)::value;
+                constexpr int PT = MM::PT(pi);
+                const int ta = cc * CK + 2 * pi;
+                if (done || ta >= T) return;
+                if (need) {  // exact words of this phase into every lane
+                    const int wi = word_at(st, pi);
+                    c0 = slot[wi];
+                    c1 = slot[wi + 64];
+                    sel = 0;
+                    need = false;
+                }
+                const uint32_t W0 = X_.readlane(c0, sel), W1 = X_.readlane(c1, sel);
+                const int qq = (st >> 8) & (Q - 1), ll = (st >> 2) & 63, bb = st >> (8 + QB), jo = st & 3;
+                if constexpr (pi > 0) {  // the next phase's four candidates (inputs h e = 0..3 of this one)
+                    const int sx = GE::start(((lane & 3) << (RB - 2)) | bb, qq, ll);
+                    const int wi = word_at(sx, pi - 1);
+                    c0 = slot[wi];
+                    c1 = slot[wi + 64];
+                }
+                const int ca = jo >> 1, cb = jo & 1;
+                const int P = MM::OFF(pi) + bb * MM::PBLK(PT);
+                const int w0 = P >> 5;
+                const uint64_t V = ((uint64_t)W0 << 32) | W1;
+                auto bits = [&](int Pp, int nbit) -> int {  // nbit bits from push Pp on, first push highest
+                    return (int)((V >> (64 - (Pp - 32 * w0) - nbit)) & ((1u << nbit) - 1u));
                 };
-                // candidate words: lane i holds the two words of hypothesis i (the input slot bits h e = i of
-                // the phase walked before) -- loaded one phase ahead; sel picks the true one
-                uint32_t c0 = 0, c1 = 0;
-                int sel = 0;
-                bool need = true;  // candidates not loaded (chunk start, or the gain slot changed)
-                uint32_t vrec = 0;
-                static_for<0, NPC>([&](auto Kc) {
-                    constexpr int pi = NPC - 1 - decltype(Kc)::value;
-                    constexpr int PT = MM::PT(pi);
-                    const int ta = cc * CK + 2 * pi;
-                    if (ta >= T || hit) return;
-                    if (need) {  // exact words of this phase into every lane
-                        const int wi = word_at(st, pi);
-                        c0 = slot[wi];
-                        c1 = slot[wi + 64];
-                        sel = 0;
-                        need = false;
-                    }
-                    const uint32_t W0 = X_.readlane(c0, sel), W1 = X_.readlane(c1, sel);
-                    const int qq = (st >> 8) & (Q - 1), ll = (st >> 2) & 63, bb = st >> (8 + QB), jo = st & 3;
-                    // prefetch the next phase's candidates (this chunk only; a new chunk starts exact)
-                    if (pi > 0 && ta > 0) {
-                        const int hyp = lane & 3;
-                        const int sx = GE::start((hyp << (RB - 2)) | bb, qq, ll);
-                        const int wi = word_at(sx, pi > 0 ? pi - 1 : 0);
-                        c0 = slot[wi];
-                        c1 = slot[wi + 64];
-                    }
-                    const int ca = jo >> 1, cb = jo & 1;
-                    const int P = MM::OFF(pi) + bb * MM::PBLK(PT);
-                    const int w0 = P >> 5;
-                    const uint64_t V = ((uint64_t)W0 << 32) | W1;
-                    auto bits = [&](int Pp, int nbit) -> int {  // nbit bits from push Pp on, first push highest
-                        return (int)((V >> (64 - (Pp - 32 * w0) - nbit)) & ((1u << nbit) - 1u));
-                    };
-                    int h = 0, e = 0, pa = 0, pb = 0;  // pa / pb: parity class of steps ta / ta + 1
-                    if constexpr (MD == 0) {
-                        e = bits(P + 2 + ca, 1);
+                int h = 0, e = 0, pa = 0, pb = 0;  // pa / pb: parity class of steps ta / ta + 1
+                if constexpr (MD == 0) {
+                    e = bits(P + 2 + ca, 1);
+                    h = bits(P + e, 1);
+                } else if constexpr (MD == 1) {
+                    const int PF = P + 2 + ca * 4;
+                    const int p = bits(PF + 2 + cb, 1);
+                    e = bits(PF + p, 1);
+                    h = bits(P + e, 1);
+                    pa = pb = p;
+                } else if constexpr (!EQ) {
+                    if constexpr (PT == 1) {  // D4 phase B: three sequential-min bits -> winner (c, b) = 0xEDEC map
+                        const int PF = P + 4 + ca * 10;
+                        const int v3 = bits(PF + 4 + 3 * cb, 3);
+                        const int idx = (0xEDEC >> (2 * v3)) & 3;
+                        cstar = idx >> 1;
+                        const int bsel = idx & 1;
+                        e = bits(PF + idx, 1);
+                        h = bits(P + 2 * e + cstar, 1);
+                        pb = bsel ^ cstar;
+                        pa = bsel;
+                    } else {  // D4 phase A, with the class chosen by the phase B that follows it
+                        const int PF = P + 2 + ca * 6;
+                        const int bsel = bits(PF + 2 + 2 * cb + cstar, 1);
+                        e = bits(PF + bsel, 1);
                         h = bits(P + e, 1);
-                    } else if constexpr (MD == 1) {
-                        const int PF = P + 2 + ca * 4;
-                        const int p = bits(PF + 2 + cb, 1);
-                        e = bits(PF + p, 1);
+                        pb = bsel ^ cstar;
+                        pa = bsel;
+                    }
+                } else {
+                    if constexpr (PT == 1) {  // EQ phase B
+                        const int PF = P + 4 + ca * 4;
+                        cstar = bits(PF + 2 + cb, 1);
+                        e = bits(PF + cstar, 1);
+                        h = bits(P + 2 * e + cstar, 1);
+                    } else {  // EQ phase A
+                        const int PF = P + 2 + ca * 2;
+                        e = bits(PF + cstar, 1);
                         h = bits(P + e, 1);
-                        pa = pb = p;
-                    } else if constexpr (!EQ) {
-                        if constexpr (PT == 1) {  // D4 phase B: three sequential-min bits -> winner (c, b) = 0xEDEC map
-                            const int PF = P + 4 + ca * 10;
-                            const int v3 = bits(PF + 4 + 3 * cb, 3);
-                            const int idx = (0xEDEC >> (2 * v3)) & 3;
-                            cstar = idx >> 1;
-                            const int bsel = idx & 1;
-                            e = bits(PF + idx, 1);
-                            h = bits(P + 2 * e + cstar, 1);
-                            pb = bsel ^ cstar;
-                            pa = bsel;
-                        } else {  // D4 phase A, with the class chosen by the phase B that follows it
-                            const int PF = P + 2 + ca * 6;
-                            const int bsel = bits(PF + 2 + 2 * cb + cstar, 1);
-                            e = bits(PF + bsel, 1);
-                            h = bits(P + e, 1);
-                            pb = bsel ^ cstar;
-                            pa = bsel;
-                        }
-                    } else {
-                        if constexpr (PT == 1) {  // EQ phase B
-                            const int PF = P + 4 + ca * 4;
-                            cstar = bits(PF + 2 + cb, 1);
-                            e = bits(PF + cstar, 1);
-                            h = bits(P + 2 * e + cstar, 1);
-                        } else {  // EQ phase A
-                            const int PF = P + 2 + ca * 2;
-                            e = bits(PF + cstar, 1);
-                            h = bits(P + e, 1);
-                        }
-                        pa = pb = cstar;
                     }
-                    const int smid = GE::mid(bb, 2 * ca + e, qq, ll);  // state at step ta
-                    const uint32_t rec2 = (uint32_t)(smid | (gs << 10) | (pa << 15)) |
-                                          ((uint32_t)(st | (gs << 10) | (pb << 15)) << 16);
-                    vrec = lane == pi ? rec2 : vrec;
-                    if (ta + 1 == midpos || ta == midpos) {
-                        if (lane == 0) a.mid_st[n] = ta + 1 == midpos ? st : smid;
-                        hit = true;
-                        return;
+                    pa = pb = cstar;
+                }
+                const int ph = ta >> 1;
+                // the phase's output state, slot, intermediate bit and classes (the step-ta state follows from them)
+                s_rec[ph] = (uint32_t)(st | (gs << 10) | (e << 14) | (pa << 15) | (pb << 16));
+                if (ph == mid_ph) {  // first tail-biting pass: only the state before mid_t is needed
+                    if (lane == 0) a.mid_st[n] = (a.mid_t - 1) & 1 ? st : GE::mid(bb, 2 * ca + e, qq, ll);
+                    done = true;
+                    return;
+                }
+                if (ta == 0) return;
+                sel = 2 * h + e;
+                st = GE::start((h << (RB - 1)) | (e << (RB - 2)) | bb, qq, ll);  // state at step ta - 1
+                if (ta == nbnd) {  // sub-block start: the path came from the slot the merge chose
+                    if (G > 1) {
+                        const int gn = (int)X_.readlane(s_gsel[jb * S + st], 0);
+                        need = gn != gs;
+                        gs = gn;
                     }
-                    if (ta == 0) return;
-                    sel = 2 * h + e;
-                    st = GE::start((h << (RB - 1)) | (e << (RB - 2)) | bb, qq, ll);  // state at step ta - 1
-                    if (ta == nbnd) {  // sub-block start: the path came from the slot the merge chose
-                        if (G > 1) {
-                            const int gn = (int)X_.readlane(s_gsel[jb * S + st], 0);
-                            need = gn != gs;
-                            gs = gn;
-                        }
-                        nbnd -= sub;
-                        jb--;
-                    }
-                });
-                const int rp = cc * NPC + lane;
-                if (lane < NPC && 2 * rp < T) s_rec[rp] = vrec;
-                if (lane == 0) s_ctl[2] = hit ? 1 : 0;
-            }
-            X_.lds_sync();
-            if (s_ctl[2]) {
-                X_.wait_loads(0);
-                store_best();
-                return;  // first tail-biting pass: only the state before mid_t is needed
-            }
-            if (cc - nslot >= 0) issue(cc - nslot);
+                    nbnd -= sub;
+                    jb--;
+                }
+            });
+            if (!done && cc - nslot >= 0) issue(cc - nslot);
         }
+        X_.wait_loads(0);  // no copy may still land in this workgroup's LDS after it ends
+        if (lane == 0) {
+            a.best[n] = bi_all;
+            if (a.end_st) a.end_st[n] = bi_all % S;
+        }
+        if (done) return;
     }
 
     // ---- reconstruction and code (tcq_viterbi.cu:662-682) -------------------------------------------
-    store_best();
     float* rn = a.rec + (size_t)n * a.ld;
-    const uint32_t* s_rec = (const uint32_t*)s_st;
-    for (int t = tid; t < T; t += nthr) {
-        const uint32_t rr = s_rec[t >> 1] >> ((t & 1) * 16);
-        const int stt = rr & 1023, gg = (rr >> 10) & 15, par = (rr >> 15) & 1;
+    for (int t = lane; t < T; t += 64) {
+        const uint32_t rr = s_rec[t >> 1];
+        const int so = rr & 1023, gg = (rr >> 10) & 15;
+        // odd step: the phase's output state; even step: its intermediate state (block bits, e, ca, q, lane of so)
+        const int stt = (t & 1) ? so
+                                : GE::mid(so >> (8 + QB), 2 * ((so >> 1) & 1) + ((rr >> 14) & 1), (so >> 8) & (Q - 1),
+                                          (so >> 2) & 63);
+        const int par = (rr >> ((t & 1) ? 16 : 15)) & 1;
         const int lb = mk.label(stt);
         const bool hi = mix > 0 && ((t / mix) & 1);
         const int Ut = hi ? U_hi : U;

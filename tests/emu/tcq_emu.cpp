@@ -59,14 +59,22 @@ struct CpuX {
         return r;
     }
     int shfl_xor(int v, int m) const { return (int)xor_lane((uint32_t)v, m); }
-    // the kernel applies it to values every lane of the wave computed identically
-    uint32_t uniform(uint32_t v) const { return v; }
+    uint32_t readlane(uint32_t v, int l) const
+    {
+        const int w = tid_ >> 6;
+        xch_[tid_] = v;
+        waves_[w]->arrive_and_wait();
+        const uint32_t r = xch_[w * 64 + l];
+        waves_[w]->arrive_and_wait();
+        return r;
+    }
     // the GPU copy is asynchronous; here it completes at once
     void load16(const uint32_t* src, uint32_t* lds_wave_base) const
     {
         std::memcpy(lds_wave_base + 4 * (tid_ & 63), src, 16);
     }
-    void wait_loads(int) const {}
+    // a wave's copies have landed for every lane once the wave has waited: model that with a wave barrier
+    void wait_loads(int) const { waves_[tid_ >> 6]->arrive_and_wait(); }
 };
 
 constexpr int kLdsMax = 160 * 1024;  // gfx950 LDS per workgroup
