@@ -41,6 +41,18 @@ int ltq_fwht256_rows(const void* x, int dtype, float* y, long rows, long cols, l
 int ltq_fwht256_cols(const float* x, float* y, long rows, long cols, long ldx, long ldy, const float* s, int smode,
                      void* stream);
 
+/* Bytes of a packed row slice [R, K] of format (fmt_K, frac, h, sub): four regions, each on a 64-byte
+ * boundary (src/ltq_file.py:67-96). Host-only arithmetic; -1 for an invalid shape. */
+long ltq_slice_bytes(int R, int K, int fmt_K, int frac, int h, int sub);
+
+/* Packs codes idx [R, K] (int16 label * U + u, row stride ld_idx) and gain indices gi [R, K] (uint8, row
+ * stride ld_gi) into the .ltq tile regions codes / planes / lsb / gains. Replaces the torch function
+ * src/ltq_file.py:79-96 (`pack_slice`, which returns the same bytes on the host) and the per-tile layout of
+ * src/ltq_format.py:104-124 (`pack_tile`). R, K multiples of 16; out holds ltq_slice_bytes(...) bytes, every
+ * one of which is written (region gaps are zero). */
+int ltq_pack_slice(const int16_t* idx, long ld_idx, const uint8_t* gi, long ld_gi, int R, int K, int fmt_K, int frac,
+                   int h, int sub, uint8_t* out, long out_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,6 +22,9 @@ SIGNATURES = {
     # FWHT-256 (src/iqk_format.py:153-170), rows with a fused scale / columns
     "ltq_fwht256_rows": (ci, [vp, ci, vp, cl, cl, cl, cl, vp, ci, vp]),
     "ltq_fwht256_cols": (ci, [vp, vp, cl, cl, cl, cl, vp, ci, vp]),
+    # .ltq slice packing (src/ltq_file.py:79-96)
+    "ltq_slice_bytes": (cl, [ci] * 6),
+    "ltq_pack_slice": (ci, [vp, cl, vp, cl, ci, ci, ci, ci, ci, ci, vp, cl, vp]),
 }
 
 

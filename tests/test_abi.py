@@ -13,7 +13,7 @@ def _declarations():
     out = {}
     for h in sorted((ROOT / "include").glob("*.h")):
         text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
-        for m in re.finditer(r"\bint\s+(\w+)\s*\(([^;{]*)\)\s*;", text):
+        for m in re.finditer(r"\b(?:int|long)\s+(\w+)\s*\(([^;{]*)\)\s*;", text):
             args = [a for a in m.group(2).replace("\n", " ").split(",") if a.strip() and a.strip() != "void"]
             out[m.group(1)] = len(args)
     return out
@@ -21,7 +21,7 @@ def _declarations():
 
 def test_header_declares_entry_points():
     decl = _declarations()
-    assert {"tcq_viterbi", "ltq_fwht256_rows", "ltq_fwht256_cols"} <= set(decl)
+    assert {"tcq_viterbi", "ltq_fwht256_rows", "ltq_fwht256_cols", "ltq_pack_slice", "ltq_slice_bytes"} <= set(decl)
     assert decl["tcq_viterbi"] == 36  # the reference's ctypes binding: 15 pointers, 18 ints, pbits, pp, stream
 
 

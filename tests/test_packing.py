@@ -1,0 +1,90 @@
+""".ltq tile packing (src/ltq_format.py:77-147, src/ltq_file.py:67-140).
+
+CPU: the oracle's numpy restatement reproduces the reference's own packed bytes and decoded values for 12
+formats (tests/golden/packing.npz), and its state / label functions match their definitions by brute force.
+GPU: the HIP packer writes the same bytes, and packing the codes of a real TCQ275X2 quantization decodes
+bit-exactly to the quantizer's reconstruction (the "0 decode mismatches" bar).
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+FORMATS = ["TCQ275X2", "TCQ275X", "TCQ375X", "TCQ25X", "TCQ3X3", "TCQ4X", "TCQ2X0", "TCQ3W2", "TCQ5X", "TCQ3X16",
+           "TCQ475X", "TCQ45X"]
+
+
+@pytest.fixture(scope="module")
+def pk(golden_dir):
+    return np.load(golden_dir / "packing.npz")
+
+
+@pytest.mark.parametrize("name", FORMATS)
+def test_oracle_pack_matches_reference_bytes(pk, name):
+    from oracle import pack
+    from ltq_amd.formats import make_format
+    f = make_format(name)
+    b = pack.pack_slice(pk[f"{name}.idx"], pk[f"{name}.gi"], f.K, f.frac, f.h, f.sub)
+    assert np.array_equal(np.frombuffer(b, np.uint8), pk[f"{name}.bytes"])
+    dec = pack.decode_slice(pk[f"{name}.bytes"], 32, 512, f.K, f.frac, f.h, f.sub, f.masks, f.lut, f.gain_tab)
+    assert np.array_equal(dec.view(np.uint32), pk[f"{name}.decoded"].view(np.uint32))
+    # per-tile fields of tile 0
+    ix = pack.tiles(pk[f"{name}.idx"].astype(np.int64))[0]
+    g = pack.tiles(pk[f"{name}.gi"].astype(np.int64))[0]
+    tf = pack.pack_tile(ix // f.U, ix % f.U, g, f.K, f.frac, f.h, f.sub)
+    for k in ("codes", "planes", "lsb", "gains"):
+        assert np.array_equal(np.asarray(tf[k]).astype(np.uint16), pk[f"{name}.tile0.{k}"]), k
+
+
+def test_oracle_state_and_label_definitions():
+    """states_from_codes is the 10-bit window of code bits ending at t (tail-biting); labels are linear."""
+    from oracle import pack
+    rng = np.random.default_rng(1)
+    c = rng.integers(0, 2, 256)
+    s = pack.states_from_codes(c)
+    for t in (0, 5, 9, 10, 200, 255):
+        assert s[t] == sum(int(c[(t - j) % 256]) << j for j in range(10))
+    masks = (359, 241, 40)
+    a, b = rng.integers(0, 1024, 64), rng.integers(0, 1024, 64)
+    la, lb, lab = (pack.labels_from_states(v, masks) for v in (a, b, a ^ b))
+    assert np.array_equal(la ^ lb, lab)
+
+
+# ---------------------------------------------------------------------------------------------- GPU
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", FORMATS)
+def test_gpu_pack_matches_reference_bytes(pk, name):
+    from ltq_amd.formats import make_format
+    from ltq_amd.ltq_file import pack_slice
+    f = make_format(name)
+    print(f"pack {name}", flush=True)
+    b = pack_slice(torch.tensor(pk[f"{name}.idx"], device="cuda"), torch.tensor(pk[f"{name}.gi"], device="cuda"), f)
+    assert np.array_equal(np.frombuffer(b, np.uint8), pk[f"{name}.bytes"])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["TCQ275X2", "TCQ25X", "TCQ3X3", "TCQ4X"])
+def test_gpu_quantize_pack_decode_roundtrip(name):
+    """Viterbi codes of a [64, 256] slice -> HIP pack -> oracle decode == the quantizer's reconstruction."""
+    from oracle import pack
+    from ltq_amd.formats import TCQ_CONFIG, make_format
+    from ltq_amd.ltq_file import pack_slice
+    from ltq_amd.tcq_proto import viterbi_ub_cuda
+    f = make_format(name)
+    cfg = TCQ_CONFIG[name]
+    R, K = 64, 256
+    g = torch.Generator().manual_seed(3)
+    W = torch.randn((R, K), generator=g) * 1.1
+    tiles = torch.tensor(pack.tiles(W.numpy()), device="cuda")  # [T, 256], position 16 r + c
+    print(f"roundtrip {name}", flush=True)
+    rec, gi, idx = viterbi_ub_cuda(tiles, torch.tensor(f.lut, device="cuda"), f.K, 10, 359,
+                                   torch.tensor(f.gain_tab, device="cuda"), sub=f.sub, tail_biting=True, tb_window=32,
+                                   m_extra=f.masks[1:], pair_parity=f.frac, n_cand=cfg.get("n_cand", 0),
+                                   return_code=True)
+    torch.cuda.synchronize()
+    idx_m = pack.untiles(idx.cpu().numpy(), R, K)
+    gi_m = pack.untiles(gi.cpu().numpy(), R, K)
+    b = pack_slice(torch.tensor(idx_m, dtype=torch.int16, device="cuda"), torch.tensor(gi_m, dtype=torch.uint8, device="cuda"), f)
+    dec = pack.decode_slice(b, R, K, f.K, f.frac, f.h, f.sub, f.masks, f.lut, f.gain_tab)
+    rec_m = pack.untiles(rec.cpu().numpy(), R, K)
+    assert np.array_equal(dec.view(np.uint32), rec_m.view(np.uint32))
