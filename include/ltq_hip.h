@@ -53,6 +53,27 @@ long ltq_slice_bytes(int R, int K, int fmt_K, int frac, int h, int sub);
 int ltq_pack_slice(const int16_t* idx, long ld_idx, const uint8_t* gi, long ld_gi, int R, int K, int fmt_K, int frac,
                    int h, int sub, uint8_t* out, long out_bytes, void* stream);
 
+/* Row scale of a rotated weight matrix w [M, K] (K % 256 == 0, row stride ldw, 16-byte aligned):
+ * rms of every 256-column block (clamped at 1e-10, times scale), d_row[M] = fp16-rounded geometric mean of
+ * the row's block rms (clamped at 1e-8), e[M, K/256] (int8, row stride lde) = clamp(round(log2(rms / d_row)
+ * / e_step), -2^(e_bits-1), 2^(e_bits-1) - 1) and d[M, K/256] (row stride ldd) = max(d_row 2^(e_step e), 1e-8).
+ * Replaces the torch code src/liqk_v2.py:938-946 (and the clamp of :959); agrees with it to fp32 rounding of
+ * the reductions and transcendental functions. */
+int ltq_row_scale(const float* w, long M, long K, long ldw, float scale, float e_step, int e_bits, float* d_row,
+                  int8_t* e, long lde, float* d, long ldd, void* stream);
+
+/* First Viterbi input of a 256-column block: x[T, 256] tiles (t = 16 r + c) = wk[:, 0:16] * (1 / d[row])
+ * (src/liqk_v2.py:955-958, the `w_sub_orig * inv_d` of sub-block 0). M % 16 == 0; d has row stride ldd. */
+int ltq_ldlq_prep(const float* wk, long ldw, const float* d, long ldd, float* x, long M, void* stream);
+
+/* LDLQ error feedback after sub-block ib (0..15) of a 256-column block (src/liqk_v2.py:957-967): G[:, 16ib..]
+ * = rec tiles, err = (wk[:, s0:s1] - d * rec) @ uinv[s0:s1, s0:s1], wk[:, s1:256] -= err @ ublk[s0:s1, s1:256],
+ * and, if xnext is not null and ib < 15, the next sub-block's Viterbi tiles xnext = wk[:, s1:s1+16] * (1 / d).
+ * wk, G: [M, 256] working copy / reconstruction of the block; uinv: the block's inverse factor (row stride
+ * ldi); ublk: the block's factor U[c0:c1, c0:c1] (row stride ldu). */
+int ltq_ldlq_sub(float* wk, long ldw, const float* rec, const float* d, long ldd, const float* uinv, long ldi,
+                 const float* ublk, long ldu, int ib, float* G, long ldg, float* xnext, long M, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

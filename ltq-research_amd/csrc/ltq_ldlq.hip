@@ -1,0 +1,148 @@
+// Row scale fitting and the LDLQ sub-block error feedback of the TCQ matrix quantizer, gfx950.
+//
+// ltq_row_scale (src/liqk_v2.py:938-946): per row, the rms of every 256-column block (clamped at 1e-10, times
+// the format scale), d_row = fp16(exp(mean over blocks of log rms)) clamped at 1e-8, the 5-bit block exponent
+// e = clamp(round(log2(rms / d_row) / e_step), -2^(bits-1), 2^(bits-1) - 1) and d = d_row * 2^(e_step e).
+// One wavefront per row. Roofline: HBM, 4 bytes read per weight.
+//
+// ltq_ldlq_sub (src/liqk_v2.py:957-967): after the Viterbi of sub-block ib of a 256-column block, for the 16
+// rows of every tile
+//     G[:, s0:s1]      = g                                   (the tile's reconstruction, unscaled)
+//     err              = (w[:, s0:s1] - d * g) @ U_inv[s0:s1, s0:s1]
+//     w[:, s1:]       -= err @ U[s0:s1, s1:]
+//     x_next           = w[:, s1:s1+16] * (1 / d)             (next sub-block's Viterbi tiles, t = 16 r + c)
+// with the element-wise products and the division rounded as the reference's torch code rounds them; the two
+// small contractions accumulate with FMAs (a library GEMM orders its sums differently as well).
+// One workgroup per tile; roofline: L2 (the block's working copy and U rows are re-read per sub-block).
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "ltq_hip.h"
+
+namespace {
+
+__global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict__ w, long M, int nblk, long ldw,
+                                                        float scale, float e_step, int e_max, float* __restrict__ d_row,
+                                                        int8_t* __restrict__ e_out, long lde, float* __restrict__ d_out,
+                                                        long ldd)
+{
+    extern __shared__ float s_rms[];  // [4 waves][nblk]
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const long row = (long)blockIdx.x * 4 + wv;
+    if (row >= M) return;
+    float* rms = s_rms + wv * nblk;
+    const float* wr = w + row * ldw;
+    float lsum = 0.f;
+    for (int b = 0; b < nblk; b++) {
+        const float4 v = *(const float4*)(wr + b * 256 + 4 * lane);
+        float s = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+        const float r = fmaxf(sqrtf(s / 256.f), 1e-10f) * scale;
+        if (lane == 0) rms[b] = r;
+        lsum += logf(r);  // every lane holds the same r
+    }
+    const float d = fmaxf(__half2float(__float2half(expf(lsum / (float)nblk))), 1e-8f);
+    if (lane == 0) d_row[row] = d;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int b = lane; b < nblk; b += 64) {
+        float e = rintf(log2f(rms[b] / d) / e_step);
+        e = fminf(fmaxf(e, (float)-e_max), (float)(e_max - 1));
+        e_out[row * lde + b] = (int8_t)e;
+        d_out[row * ldd + b] = fmaxf(d * exp2f(e_step * e), 1e-8f);
+    }
+}
+
+__global__ __launch_bounds__(256) void ldlq_sub_kernel(float* __restrict__ wk, long ldw, const float* __restrict__ rec,
+                                                       const float* __restrict__ d, long ldd,
+                                                       const float* __restrict__ uinv, long ldi,
+                                                       const float* __restrict__ ublk, long ldu, int s0,
+                                                       float* __restrict__ G, long ldg,
+                                                       float* __restrict__ xnext, long M)
+{
+    __shared__ float s_err[16][17];
+    __shared__ float s_d[16];
+    const int tid = threadIdx.x, r = tid >> 4, c = tid & 15;
+    const long row0 = (long)blockIdx.x * 16, row = row0 + r;
+    if (row0 >= M) return;
+    const int s1 = s0 + 16;
+    if (tid < 16) s_d[tid] = d[(row0 + tid) * ldd];
+    // tile element t = 16 r + c is row r, sub-block column c
+    const float g = rec[(long)blockIdx.x * 256 + tid];
+    G[row * ldg + s0 + c] = g;
+    __syncthreads();
+    const float dr = s_d[r];
+    // residual of this element, then err[r][c] = sum_k resid[r][k] * uinv[s0+k][s0+c]
+    const float resid = wk[row * ldw + s0 + c] - dr * g;
+    s_err[r][c] = resid;
+    __syncthreads();
+    float e = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) e = __fmaf_rn(s_err[r][k], uinv[(long)(s0 + k) * ldi + s0 + c], e);
+    __syncthreads();
+    s_err[r][c] = e;
+    __syncthreads();
+    // w[r][j] -= sum_k err[r][k] * U[s0+k][j] for j >= s1: thread (r, c) updates columns s1 + c, s1 + c + 16, ...
+    for (int j = s1 + c; j < 256; j += 16) {
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; k++) acc = __fmaf_rn(s_err[r][k], ublk[(long)(s0 + k) * ldu + j], acc);
+        wk[row * ldw + j] -= acc;
+    }
+    if (xnext && s1 < 256) {
+        const float inv = 1.0f / dr;
+        xnext[(long)blockIdx.x * 256 + tid] = wk[row * ldw + s1 + c] * inv;
+    }
+}
+
+// first sub-block's tiles of a block: x[t = 16 r + c] = w[r][c] * (1 / d[r])
+__global__ __launch_bounds__(256) void ldlq_prep_kernel(const float* __restrict__ wk, long ldw, const float* __restrict__ d,
+                                                        long ldd, float* __restrict__ x, long M)
+{
+    const int tid = threadIdx.x, r = tid >> 4, c = tid & 15;
+    const long row = (long)blockIdx.x * 16 + r;
+    if (row >= M) return;
+    const float inv = 1.0f / d[row * ldd];
+    x[(long)blockIdx.x * 256 + tid] = wk[row * ldw + c] * inv;
+}
+
+}  // namespace
+
+extern "C" int ltq_row_scale(const float* w, long M, long K, long ldw, float scale, float e_step, int e_bits,
+                             float* d_row, int8_t* e, long lde, float* d, long ldd, void* stream)
+{
+    if (M < 0 || K < 0 || K % 256 || ldw < K || (ldw & 3) || e_bits < 1 || e_bits > 8 || !(e_step > 0.f) || !(scale > 0.f))
+        return -1;
+    const int nblk = (int)(K / 256);
+    if (M == 0 || nblk == 0) return 0;
+    if (!w || !d_row || !e || !d || lde < nblk || ldd < nblk || ((uintptr_t)w & 15) || nblk > 4096) return -1;
+    const long grid = (M + 3) / 4;
+    hipLaunchKernelGGL(row_scale_kernel, dim3((unsigned)grid), dim3(256), 4 * 4 * nblk, (hipStream_t)stream, w, M, nblk,
+                       ldw, scale, e_step, 1 << (e_bits - 1), d_row, e, lde, d, ldd);
+    return (int)hipGetLastError();
+}
+
+extern "C" int ltq_ldlq_prep(const float* wk, long ldw, const float* d, long ldd, float* x, long M, void* stream)
+{
+    if (M < 0 || M % 16 || ldw < 16 || ldd < 1) return -1;
+    if (M == 0) return 0;
+    if (!wk || !d || !x) return -1;
+    hipLaunchKernelGGL(ldlq_prep_kernel, dim3((unsigned)(M / 16)), dim3(256), 0, (hipStream_t)stream, wk, ldw, d, ldd, x, M);
+    return (int)hipGetLastError();
+}
+
+extern "C" int ltq_ldlq_sub(float* wk, long ldw, const float* rec, const float* d, long ldd, const float* uinv,
+                            long ldi, const float* ublk, long ldu, int ib, float* G, long ldg, float* xnext, long M,
+                            void* stream)
+{
+    if (M < 0 || M % 16 || ib < 0 || ib > 15 || ldw < 256 || ldi < 256 || ldu < 256 || ldg < 256 || ldd < 1) return -1;
+    if (M == 0) return 0;
+    if (!wk || !rec || !d || !uinv || !ublk || !G) return -1;
+    hipLaunchKernelGGL(ldlq_sub_kernel, dim3((unsigned)(M / 16)), dim3(256), 0, (hipStream_t)stream, wk, ldw, rec, d, ldd,
+                       uinv, ldi, ublk, ldu, 16 * ib, G, ldg, xnext, M);
+    return (int)hipGetLastError();
+}
