@@ -49,41 +49,33 @@ def student_t(shape, gen, dev):
 
 
 def prepare(dev, rows=M_ROWS, cols=K_COLS):
-    """Inputs of the quantizer on the device: Viterbi tiles [nblk, 16, rows/16, 256] (x / d per row block,
-    tile-major), per-position weights [nblk, 16, 256] (diag_w of the sub-block repeated over 16 rows)."""
+    """W [rows, cols] bf16 and H [cols, cols] fp32 on the device (seeded device generators: W 0, activations 1;
+    outlier columns: seed 2 on the CPU)."""
     import torch
-    from ltq_amd.formats import TCQ_CONFIG
-    from ltq_amd import rotation
-
-    # seeded device generators (W: 0, activations: 1, outlier columns: 2 on the CPU)
     W = student_t((rows, cols), torch.Generator(device=dev).manual_seed(0), dev) * 0.02
     cols_out = torch.randperm(cols, generator=torch.Generator().manual_seed(2))[:max(1, cols * N_OUTLIER // K_COLS)]
     W[:, cols_out.to(dev)] *= 20
     W = W.to(torch.bfloat16)
     X = torch.randn((N_ACT, cols), generator=torch.Generator(device=dev).manual_seed(1), device=dev)
     H = (X.T @ X) / N_ACT
-    del X
-    W_rot, H_rot, suh = rotation.compute_optimal_suh(W, H, seed=1337)
-    del H
-    H_rot.diagonal().add_(DAMP * H_rot.diagonal().mean().clamp(min=1e-8))
-    L_flip = torch.linalg.cholesky(H_rot.flip(0, 1))
-    del H_rot
-    U = torch.linalg.solve_triangular(L_flip, torch.eye(cols, device=dev), upper=False).flip(0, 1)
-    del L_flip
-    diag_w = 1.0 / (torch.diagonal(U) ** 2).clamp(min=1e-12)
-    del U
+    return W, H
+
+
+def sample_tiles(W, H, nsub):
+    """Viterbi tiles and weights of the first nsub sub-blocks (block 0, no LDLQ feedback yet applied beyond the
+    first sub-block) for the CPU baseline: rotation, row scale and factors as the GPU step computes them."""
+    import torch
+    from ltq_amd import liqk, rotation
+    from ltq_amd.formats import TCQ_CONFIG
     cfg = TCQ_CONFIG[FORMAT]
-    nblk = cols // 256
-    # row scale (src/liqk_v2.py:938-946)
-    rms_rb = W_rot.view(rows, nblk, 256).square().mean(dim=2).sqrt().clamp(min=1e-10) * cfg.get("scale", 1.0)
-    d_row = torch.exp(torch.log(rms_rb).mean(dim=1)).to(torch.float16).to(torch.float32).clamp(min=1e-8)
-    e_rb = torch.round(torch.log2(rms_rb / d_row.unsqueeze(1)) / 0.25).clamp(-16, 15)
-    d_rb = (d_row.unsqueeze(1) * torch.exp2(0.25 * e_rb)).clamp(min=1e-8)
-    xs = W_rot.view(rows, nblk, 16, 16) / d_rb.view(rows, nblk, 1, 1)
-    # tile n of sub-block (b, s) = rows 16n..16n+15, columns 16s..16s+15 of block b, row-major in the tile
-    tiles = xs.view(rows // 16, 16, nblk, 16, 16).permute(2, 3, 0, 1, 4).contiguous().view(nblk, 16, rows // 16, 256)
-    wts = diag_w.view(nblk, 16, 16).repeat(1, 1, 16).contiguous()
-    return tiles, wts
+    W_rot, H_rot, _ = rotation.compute_optimal_suh(W.float(), H.float(), seed=1337)
+    _, diag_w, _ = liqk.factor_hessian(H_rot, DAMP)
+    _, _, d = liqk.row_scale(W_rot, cfg)
+    rows = W.shape[0]
+    xs = W_rot[:, :256].view(rows, 16, 16) / d[:, 0].view(rows, 1, 1)
+    tiles = xs.view(rows // 16, 16, 16, 16).permute(2, 0, 1, 3).contiguous().view(16, rows // 16, 256)
+    wts = diag_w[:256].view(16, 16).repeat(1, 16).contiguous()
+    return tiles[:nsub].cpu(), wts[:nsub].cpu()
 
 
 def lane_ops_per_launch(cfg, tiles, steps):
@@ -113,9 +105,9 @@ def cpu_baseline(tiles, wts, budget_s):
     ref.lib()
     done, t0 = 0, time.perf_counter()
     nsub = 0
-    for b, s in ((b, s) for b in range(tiles.shape[0]) for s in range(tiles.shape[1])):
-        x = tiles[b, s].cpu().numpy()
-        w = wts[b, s].cpu().numpy()
+    for s in range(tiles.shape[0]):
+        x = tiles[s].numpy()
+        w = wts[s].numpy()
         ref.viterbi_ub_cuda_ref(x, f.lut, f.K, 10, 359, f.gain_tab, sub=f.sub, wts=w, n_cand=cfg.get("n_cand", 0),
                                 tail_biting=True, tb_window=TB_WINDOW, m_extra=f.masks[1:], pair_parity=int(cfg["pp"]),
                                 return_code=True, nthreads=cores)
@@ -126,7 +118,7 @@ def cpu_baseline(tiles, wts, budget_s):
     dt = time.perf_counter() - t0
     return {"value": round(done / dt / 1e6, 4), "unit": "Mweights/s", "cores": cores, "kind": "port",
             "sample": f"oracle/ltq_oracle.c two-pass tail-biting Viterbi of the first {nsub} sub-block(s) in order "
-                      f"({nsub} x {tiles.shape[2]} tiles x 256 weights = {done} weights) in {dt:.1f} s on {cores} threads"}
+                      f"({nsub} x {tiles.shape[1]} tiles x 256 weights = {done} weights) in {dt:.1f} s on {cores} threads"}
 
 
 def main():
@@ -135,18 +127,20 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample (0 = skip)")
-    ap.add_argument("--blocks", type=int, default=0, help="column blocks per step (0 = all 56; profiling runs only)")
+    ap.add_argument("--cols", type=int, default=K_COLS, help="matrix columns (profiling runs may use fewer)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="profiling runs: first copy this many MiB device-to-device (a known-size kernel that "
                          "calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU only: the Viterbi path is row-sharded with no exchange on the hot path, "
+        print("bench.py measures one GPU only: the quantizer is row-sharded with no exchange on the hot path, "
               "and this build runs and reports a single MI355X (--gpus 1).", file=sys.stderr)
         sys.exit(2)
+    if args.cols % 256 or args.cols <= 0:
+        sys.exit("--cols must be a positive multiple of 256")
 
     import torch
-    from ltq_amd import tcq_proto
+    from ltq_amd import liqk, ltq_file, tcq_proto
     from ltq_amd.formats import TCQ_CONFIG, make_format
 
     dev = torch.device("cuda:0")
@@ -158,75 +152,85 @@ def main():
         torch.empty_like(a).copy_(a)
         torch.cuda.synchronize()
         del a
-    tiles, wts = prepare(dev)
-    nblk = args.blocks or tiles.shape[0]
-    lut = torch.tensor(f.lut, device=dev)
-    gains = torch.tensor(f.gain_tab, device=dev)
-    n_cand = cfg.get("n_cand", 0)
-    kw = dict(sub=f.sub, n_cand=n_cand, m_extra=f.masks[1:], pair_parity=int(cfg["pp"]))
-    h = 128
+    W, H = prepare(dev, cols=args.cols)
+    rows, cols = W.shape
     stream = torch.cuda.current_stream()
 
-    def step(events=None):
-        codes = []
-        for b in range(nblk):
-            for s in range(16):
-                x, w = tiles[b, s], wts[b, s]
-                # pass 1: window [h - 32, h + 32) for the middle state; pass 2: closed path from it
-                # (the two passes of src/tcq_proto.py:584-609, issued individually to time each launch)
-                if events is not None:
-                    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-                    e[0].record(stream)
-                _, mid = tcq_proto.viterbi_ub_cuda(x, lut, f.K, 10, 359, gains, wts=w.view(1, 256).expand(x.shape[0], 256),
-                                                   _mid=TB_WINDOW, _steps=2 * TB_WINDOW, _rot=h - TB_WINDOW, **kw)
-                if events is not None:
-                    e[1].record(stream)
-                out = tcq_proto.viterbi_ub_cuda(x, lut, f.K, 10, 359, gains, wts=w.view(1, 256).expand(x.shape[0], 256),
-                                                init_state=mid, return_code=True, _tail=True, _rot=h, **kw)
-                if events is not None:
-                    e[2].record(stream)
-                    events.append(e)
-                codes.append(out[2])
-        return codes
+    def step():
+        """W (bf16, HBM) and H -> rotation, suh, factors, row scale, LDLQ + Viterbi, refit, packed .ltq slice."""
+        liqk.PACK = {}
+        try:
+            q, _, rel = liqk.quantize_matrix_liqk_v2(W, H, FORMAT, damp=DAMP / 10)
+            pm = liqk.PACK["matrix"]
+        finally:
+            liqk.PACK = None
+        packed = ltq_file.pack_slice_device(pm["idx"], pm["gi"], f)
+        liqk._mark("pack")
+        return packed, pm, q, rel
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    events = []
+    liqk.STAGE_EVENTS, tcq_proto.LAUNCH_EVENTS = [], []
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
+    e0.record(stream)
     for _ in range(args.steps):
-        step(events)
+        packed, pm, q, rel = step()
+    e1.record(stream)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    ms_step = dt / args.steps * 1e3
-    weights = nblk * 16 * tiles.shape[2] * 256
-    value = weights / (dt / args.steps) / 1e6
+    stage_ev, launch_ev = liqk.STAGE_EVENTS, tcq_proto.LAUNCH_EVENTS
+    liqk.STAGE_EVENTS = tcq_proto.LAUNCH_EVENTS = None
 
-    t_p1 = sum(e[0].elapsed_time(e[1]) for e in events) / len(events) * 1e-3
-    t_p2 = sum(e[1].elapsed_time(e[2]) for e in events) / len(events) * 1e-3
-    ntile = tiles.shape[2]
+    ms_step = dt / args.steps * 1e3
+    weights = rows * cols
+    value = weights / (dt / args.steps) / 1e6
+    # stage durations (per step, ms): consecutive marks start, rotation, factor, rows, refit, pack
+    stages = {}
+    for i in range(1, len(stage_ev)):
+        name, ev = stage_ev[i]
+        if name == "start":
+            continue
+        stages[name] = stages.get(name, 0.0) + stage_ev[i - 1][1].elapsed_time(ev) / args.steps
+    durs = [a.elapsed_time(b) * 1e-3 for a, b in launch_ev]
+    t_vit = sum(durs) / args.steps
+    # tail-biting: launches alternate pass 1 (2 * tb_window steps) and pass 2 (256 steps) over rows / 16 tiles
+    d1, d2 = durs[0::2], durs[1::2]
+    t_p1, t_p2 = sum(d1) / len(d1), sum(d2) / len(d2)
+    ntile = rows // 16
     ops = (lane_ops_per_launch(cfg, ntile, 2 * TB_WINDOW) + lane_ops_per_launch(cfg, ntile, 256)) / 2
     avg = (t_p1 + t_p2) / 2
     achieved = ops / avg / 1e12
     traffic = read_traffic()
+    t_mat = sum(stages.get(k, 0.0) for k in ("rotation", "rows", "pack")) * 1e-3
     out = {
         "metric": "Mweights/s quantized (K=3 D4, 4096x14336) on 1 GPU; % VALU ACS roofline",
         "value": round(value, 3), "unit": "Mweights/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic, generated on the device (Student-t(5)*0.02 bf16 weights, 143 outlier "
                                 "columns x20; H from 2048 N(0,1) rows; seeds 0/1/2)",
-        "config": {"workload": f"C3 down_proj {M_ROWS}x{K_COLS} {FORMAT} (K=3 D4, nl=8, h=2) tail-biting "
-                               f"tb_window={TB_WINDOW}, Viterbi of all {nblk * 16} sub-blocks per step "
-                               f"({ntile} tiles per launch, 2 passes)",
-                   "stages_timed": ["viterbi_tail_biting"], "format": FORMAT, "rows": M_ROWS,
-                   "cols": nblk * 256, "parallelism": "single GPU"},
+        "config": {"workload": f"C3 down_proj {rows}x{cols} {FORMAT} (K=3 D4, nl=8, h=2) tail-biting "
+                               f"tb_window={TB_WINDOW}, damping {DAMP} mean(diag H_rot), LDLQ on: one step = "
+                               f"quantize_matrix_liqk_v2 with PACK (rotation, factors, row scale, "
+                               f"{cols // 256 * 16} two-pass Viterbi sub-blocks of {ntile} tiles, LDLQ, refit) + "
+                               f".ltq slice packing",
+                   "format": FORMAT, "rows": rows, "cols": cols, "parallelism": "single GPU"},
         "roofline": {"bound": "valu", "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
                      "unit": "TFLOP/s (fp32 VALU lane-ops/s x 1e-12)", "frac": round(achieved / VALU_PEAK_TOPS, 4),
-                     "traffic": traffic, "kernel": "tcq_viterbi_kernel<10,2,8,4>",
+                     "traffic": traffic, "kernel": "tcq_viterbi_kernel<10,2,2,8>",
                      "avg_launch_us": round(avg * 1e6, 2), "pass1_us": round(t_p1 * 1e6, 2),
                      "pass2_us": round(t_p2 * 1e6, 2), "lane_ops_per_launch": ops},
+        "breakdown": {"stages_ms": {k: round(v, 3) for k, v in stages.items()},
+                      "t_mat_ms": round(t_mat * 1e3, 3), "mweights_s_t_mat": round(weights / t_mat / 1e6, 3),
+                      "t_vit_ms": round(t_vit * 1e3, 3), "mweights_s_viterbi": round(weights / t_vit / 1e6, 3),
+                      "viterbi_launches_per_step": len(durs) // args.steps, "proxy_rel_loss": round(rel, 6),
+                      "packed_bytes": int(packed.numel())},
     }
     if args.cpu_seconds > 0:
+        nsub = 16
+        tiles, wts = sample_tiles(W, H, nsub)
         out["cpu_baseline"] = cpu_baseline(tiles, wts, args.cpu_seconds)
     print(json.dumps(out), flush=True)
 

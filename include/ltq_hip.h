@@ -70,9 +70,13 @@ int ltq_ldlq_prep(const float* wk, long ldw, const float* d, long ldd, float* x,
  * = rec tiles, err = (wk[:, s0:s1] - d * rec) @ uinv[s0:s1, s0:s1], wk[:, s1:256] -= err @ ublk[s0:s1, s1:256],
  * and, if xnext is not null and ib < 15, the next sub-block's Viterbi tiles xnext = wk[:, s1:s1+16] * (1 / d).
  * wk, G: [M, 256] working copy / reconstruction of the block; uinv: the block's inverse factor (row stride
- * ldi); ublk: the block's factor U[c0:c1, c0:c1] (row stride ldu). */
+ * ldi); ublk: the block's factor U[c0:c1, c0:c1] (row stride ldu). If code (the Viterbi's int32 codes
+ * [M/16, 256], gain index << 16 | level index) is not null, the PACK fields of the sub-block are written as
+ * well: idx[:, s0:s1] = code & 0xFFFF (int16, row stride ld_idx) and gi[:, s0:s1] = code >> 16 (uint8, row
+ * stride ld_gi), the torch scatter of src/liqk_v2.py:919-921; idx and gi point at the block's first column. */
 int ltq_ldlq_sub(float* wk, long ldw, const float* rec, const float* d, long ldd, const float* uinv, long ldi,
-                 const float* ublk, long ldu, int ib, float* G, long ldg, float* xnext, long M, void* stream);
+                 const float* ublk, long ldu, int ib, float* G, long ldg, float* xnext, long M, const int* code,
+                 int16_t* idx, long ld_idx, uint8_t* gi, long ld_gi, void* stream);
 
 #ifdef __cplusplus
 }

@@ -11,6 +11,7 @@
 //     err              = (w[:, s0:s1] - d * g) @ U_inv[s0:s1, s0:s1]
 //     w[:, s1:]       -= err @ U[s0:s1, s1:]
 //     x_next           = w[:, s1:s1+16] * (1 / d)             (next sub-block's Viterbi tiles, t = 16 r + c)
+//     idx[:, s0:s1]    = code & 0xFFFF, gi[:, s0:s1] = code >> 16   (optional: the PACK fields, src/liqk_v2.py:919-921)
 // with the element-wise products and the division rounded as the reference's torch code rounds them; the two
 // small contractions accumulate with FMAs (a library GEMM orders its sums differently as well).
 // One workgroup per tile; roofline: L2 (the block's working copy and U rows are re-read per sub-block).
@@ -62,7 +63,9 @@ __global__ __launch_bounds__(256) void ldlq_sub_kernel(float* __restrict__ wk, l
                                                        const float* __restrict__ uinv, long ldi,
                                                        const float* __restrict__ ublk, long ldu, int s0,
                                                        float* __restrict__ G, long ldg,
-                                                       float* __restrict__ xnext, long M)
+                                                       float* __restrict__ xnext, long M,
+                                                       const int* __restrict__ code, int16_t* __restrict__ idx,
+                                                       long ld_idx, uint8_t* __restrict__ gi, long ld_gi)
 {
     __shared__ float s_err[16][17];
     __shared__ float s_d[16];
@@ -74,6 +77,11 @@ __global__ __launch_bounds__(256) void ldlq_sub_kernel(float* __restrict__ wk, l
     // tile element t = 16 r + c is row r, sub-block column c
     const float g = rec[(long)blockIdx.x * 256 + tid];
     G[row * ldg + s0 + c] = g;
+    if (code) {
+        const int cv = code[(long)blockIdx.x * 256 + tid];
+        idx[row * ld_idx + s0 + c] = (int16_t)(cv & 0xFFFF);
+        gi[row * ld_gi + s0 + c] = (uint8_t)(cv >> 16);
+    }
     __syncthreads();
     const float dr = s_d[r];
     // residual of this element, then err[r][c] = sum_k resid[r][k] * uinv[s0+k][s0+c]
@@ -137,12 +145,13 @@ extern "C" int ltq_ldlq_prep(const float* wk, long ldw, const float* d, long ldd
 
 extern "C" int ltq_ldlq_sub(float* wk, long ldw, const float* rec, const float* d, long ldd, const float* uinv,
                             long ldi, const float* ublk, long ldu, int ib, float* G, long ldg, float* xnext, long M,
-                            void* stream)
+                            const int* code, int16_t* idx, long ld_idx, uint8_t* gi, long ld_gi, void* stream)
 {
     if (M < 0 || M % 16 || ib < 0 || ib > 15 || ldw < 256 || ldi < 256 || ldu < 256 || ldg < 256 || ldd < 1) return -1;
+    if (code && (!idx || !gi || ld_idx < 256 || ld_gi < 256)) return -1;
     if (M == 0) return 0;
     if (!wk || !rec || !d || !uinv || !ublk || !G) return -1;
     hipLaunchKernelGGL(ldlq_sub_kernel, dim3((unsigned)(M / 16)), dim3(256), 0, (hipStream_t)stream, wk, ldw, rec, d, ldd,
-                       uinv, ldi, ublk, ldu, 16 * ib, G, ldg, xnext, M);
+                       uinv, ldi, ublk, ldu, 16 * ib, G, ldg, xnext, M, code, idx, ld_idx, gi, ld_gi);
     return (int)hipGetLastError();
 }

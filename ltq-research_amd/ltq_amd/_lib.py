@@ -28,7 +28,7 @@ SIGNATURES = {
     # row scale and LDLQ sub-block feedback (src/liqk_v2.py:938-967)
     "ltq_row_scale": (ci, [vp, cl, cl, cl, cf, cf, ci, vp, vp, cl, vp, cl, vp]),
     "ltq_ldlq_prep": (ci, [vp, cl, vp, cl, vp, cl, vp]),
-    "ltq_ldlq_sub": (ci, [vp, cl, vp, vp, cl, vp, cl, vp, cl, ci, vp, cl, vp, cl, vp]),
+    "ltq_ldlq_sub": (ci, [vp, cl, vp, vp, cl, vp, cl, vp, cl, ci, vp, cl, vp, cl, vp, vp, cl, vp, cl, vp]),
 }
 
 

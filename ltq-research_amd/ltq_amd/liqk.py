@@ -10,8 +10,8 @@ Mirrors (same names, argument meaning, results and the module-level PACK switch)
                                                        tcq_viterbi two-pass tail-biting, library GEMM across blocks)
   quantize_matrix_liqk_v2     src/liqk_v2.py:1029-1200 (single TCQ spec or TCQ row slices; refit and PACK tail)
 
-The dense linear algebra (Cholesky, triangular solves, the inter-block error GEMM, the refit products and
-solve) runs through torch on the device, i.e. rocSOLVER / hipBLASLt on MI355X.
+The dense linear algebra (Cholesky, triangular inverse and solves, the inter-block error GEMM, the refit
+products) runs on the device through ltq_amd.linalg and torch, i.e. as large hipBLASLt / rocBLAS GEMMs.
 """
 from __future__ import annotations
 
@@ -20,12 +20,22 @@ from typing import Dict, List, Optional, Tuple
 
 import torch
 
-from . import _lib, rotation
+from . import _lib, linalg, rotation
 from .formats import QK_K, SUBBLOCK_SIZE, TCQ_CONFIG
 from .tcq_proto import make_gains, viterbi_ub_cuda
 
 PACK: Optional[dict] = None
+# timing hook (off by default): a list receives (stage name, torch.cuda.Event) at every stage boundary of
+# quantize_matrix_liqk_v2, recorded on the stream the kernels run on
+STAGE_EVENTS: Optional[list] = None
 NUM_SUBBLOCKS = QK_K // SUBBLOCK_SIZE
+
+
+def _mark(name: str) -> None:
+    if STAGE_EVENTS is not None:
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record(torch.cuda.current_stream())
+        STAGE_EVENTS.append((name, ev))
 
 
 def _check(rc: int, what: str) -> None:
@@ -43,10 +53,11 @@ def factor_hessian(H_rot: torch.Tensor, damp: float) -> Tuple[torch.Tensor, torc
     H_reg = H_rot.float().clone()
     diag_mean = H_reg.diagonal().mean().clamp(min=1e-8)
     H_reg.diagonal().add_(damp * diag_mean)
-    L_flip = torch.linalg.cholesky(H_reg.flip(0, 1))
+    L_flip, info = linalg.cholesky_lower(H_reg.flip(0, 1).contiguous())
     del H_reg
-    U = torch.linalg.solve_triangular(L_flip, torch.eye(K, dtype=L_flip.dtype, device=L_flip.device), upper=False)
-    U = U.flip(0, 1).contiguous()  # the kernels take row-major factors
+    if int(info.item()) != 0:
+        raise torch.linalg.LinAlgError("factor_hessian: the damped Hessian is not positive definite")
+    U = linalg.tri_inv_lower(L_flip).flip(0, 1).contiguous()  # the kernels take row-major factors
     del L_flip
     diag_w = 1.0 / (torch.diagonal(U) ** 2).clamp(min=1e-12)
     eye = torch.eye(QK_K, dtype=torch.float32, device=H_rot.device).unsqueeze(0).expand(nblocks, -1, -1)
@@ -109,7 +120,7 @@ def _quantize_rows_tcq_ldlq(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: to
     stream = _lib.stream_ptr()
     x_cur = torch.empty((nt, QK_K), dtype=torch.float32, device=device)
     x_nxt = torch.empty_like(x_cur)
-    G_pass = torch.empty((M, QK_K), dtype=torch.float32, device=device)
+    G_buf = torch.empty((M, QK_K), dtype=torch.float32, device=device) if pk is None else None
     for ibl in range(nblocks):
         c0, c1 = ibl * QK_K, (ibl + 1) * QK_K
         w_blk_start = W_work[:, c0:c1].clone()
@@ -118,33 +129,35 @@ def _quantize_rows_tcq_ldlq(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: to
         U_blk_inv = U_blks_inv[ibl]
         diag_w_blk = diag_w[c0:c1]
         d_rb = d_rb_all[:, ibl]
+        # per-position weights of every sub-block's tiles (t = 16 r + c -> diag_w[s0 + c]), once per block
+        wts_blk = diag_w_blk.view(NUM_SUBBLOCKS, 1, 1, SUBBLOCK_SIZE).expand(NUM_SUBBLOCKS, nt, 16, SUBBLOCK_SIZE)
+        wts_blk = wts_blk.reshape(NUM_SUBBLOCKS, nt, 16 * SUBBLOCK_SIZE)
+        G_pass = G_buf if pk is None else pk["G"][:, c0:c1]
+        codes = (pk["idx"][:, c0:], pk["idx"].stride(0), pk["gi"][:, c0:], pk["gi"].stride(0)) if pk else None
         _check(lib.ltq_ldlq_prep(w_sub_work.data_ptr(), QK_K, d_rb.data_ptr(), nblocks, x_cur.data_ptr(), M, stream),
                "ltq_ldlq_prep")
         for ib in range(NUM_SUBBLOCKS):
             s0, s1 = ib * SUBBLOCK_SIZE, (ib + 1) * SUBBLOCK_SIZE
-            out = viterbi_ub_cuda(x_cur, lut, cfg["K"], cfg["nu"], cfg["m"], gains, sub=sub,
-                                  wts=diag_w_blk[s0:s1].repeat(16), n_cand=n_cand, tail_biting=True,
-                                  tb_window=tb_window, m_extra=cfg.get("m_extra", ()),
-                                  pair_parity=cfg.get("pp", False), return_code=pk is not None)
-            if pk is not None:
-                rec, gi, ix = out
-                pk["gi"][:, c0 + s0:c0 + s1] = gi.reshape(M, SUBBLOCK_SIZE).to(torch.uint8)
-                pk["idx"][:, c0 + s0:c0 + s1] = ix.reshape(M, SUBBLOCK_SIZE).to(torch.int16)
-            else:
-                rec = out
+            out = viterbi_ub_cuda(x_cur, lut, cfg["K"], cfg["nu"], cfg["m"], gains, sub=sub, wts=wts_blk[ib],
+                                  n_cand=n_cand, tail_biting=True, tb_window=tb_window,
+                                  m_extra=cfg.get("m_extra", ()), pair_parity=cfg.get("pp", False),
+                                  return_code=pk is not None, _raw_code=True)
+            rec, code = out if pk is not None else (out, None)
+            # G, the error feedback, the next sub-block's tiles and (PACK) the code / gain index scatter
             _check(lib.ltq_ldlq_sub(w_sub_work.data_ptr(), QK_K, rec.data_ptr(), d_rb.data_ptr(), nblocks,
                                     U_blk_inv.data_ptr(), U_blk_inv.stride(0), U_blk.data_ptr(), U_blk.stride(0), ib,
-                                    G_pass.data_ptr(), QK_K, x_nxt.data_ptr() if s1 < QK_K else None, M, stream),
+                                    G_pass.data_ptr(), G_pass.stride(0), x_nxt.data_ptr() if s1 < QK_K else None, M,
+                                    code.data_ptr() if code is not None else None,
+                                    codes[0].data_ptr() if codes else None, codes[1] if codes else 0,
+                                    codes[2].data_ptr() if codes else None, codes[3] if codes else 0, stream),
                    "ltq_ldlq_sub")
             x_cur, x_nxt = x_nxt, x_cur
         best_what_row = d_rb.unsqueeze(1) * G_pass
         W_hat_rot[:, c0:c1] = best_what_row
-        if pk is not None:
-            pk["G"][:, c0:c1] = G_pass
         d_full[:, ibl] = d_rb.to(torch.float16)
         if c1 < K:
             err_blk = (w_blk_start - best_what_row) @ U_blk_inv
-            W_work[:, c1:] -= err_blk @ U[c0:c1, c1:]
+            W_work[:, c1:].addmm_(err_blk, U[c0:c1, c1:], alpha=-1.0)
     if pk is not None:
         PACK["groups"].append({"spec": spec_name, "d_row": d_row, "e": e_rb, "idx": pk["idx"], "gi": pk["gi"],
                                "G": pk["G"]})
@@ -182,9 +195,12 @@ def quantize_matrix_liqk_v2(W: torch.Tensor, H: torch.Tensor, spec_or_row_specs,
             raise NotImplementedError(f"{sp}: only TCQ formats are quantized on the GPU path")
     damp *= float(os.environ.get("TCQ_DAMP_MULT", "10"))
 
+    _mark("start")
     W_rot, H_rot, suh = rotation.compute_optimal_suh(W_f32, H_f32, seed=seed, row_weights=row_weights)
+    _mark("rotation")
     U, diag_w, U_blks_inv = factor_hessian(H_rot, damp)
     del H_rot
+    _mark("factor")
 
     row_slices = [(0, M, spec_or_row_specs)] if isinstance(spec_or_row_specs, str) else spec_or_row_specs
     by_spec: Dict[str, List[Tuple[int, int]]] = {}
@@ -209,6 +225,7 @@ def quantize_matrix_liqk_v2(W: torch.Tensor, H: torch.Tensor, spec_or_row_specs,
             g = PACK["groups"].pop()
             for k in ("idx", "gi", "G", "d_row", "e"):
                 pm[k][rows_idx] = g[k].to(pm[k].dtype)
+    _mark("rows")
 
     # ---- c_row / suh refit (src/liqk_v2.py:1139-1180) ----------------------------------------------------
     U_base = rotation.fwht_inplace(W_hat_rot.clone(), block_size=QK_K)
@@ -232,7 +249,7 @@ def quantize_matrix_liqk_v2(W: torch.Tensor, H: torch.Tensor, spec_or_row_specs,
     b_in = (U_w * HW).sum(dim=0)
     A_in.diagonal().add_(1e-3 * A_in.diagonal().mean().clamp(min=1e-12))
     try:
-        suh_cand = torch.linalg.solve(A_in, b_in).to(torch.float16).to(torch.float32)
+        suh_cand = linalg.spd_solve(A_in, b_in).to(torch.float16).to(torch.float32)
         valid_s = torch.isfinite(suh_cand) & (suh_cand.abs() > 0.05) & (suh_cand.abs() < 10.0)
         suh_cand = torch.where(valid_s, suh_cand, suh)
         W_hat_cand = U_scaled * suh_cand.unsqueeze(0)
@@ -266,4 +283,5 @@ def quantize_matrix_liqk_v2(W: torch.Tensor, H: torch.Tensor, spec_or_row_specs,
     den_loss = float((HW * W_f32).sum().clamp(min=1e-12).item())
     rel_loss = num_loss / den_loss
     qdata_out = {"d": d_full, "suh": suh.to(torch.float16), "row_slices": row_slices}
+    _mark("refit")
     return qdata_out, W_hat_eff, rel_loss

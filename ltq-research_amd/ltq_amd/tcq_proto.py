@@ -13,6 +13,10 @@ import torch
 
 from . import _lib
 
+# timing hook (off by default): a list receives one (start, end) torch.cuda.Event pair per tcq_viterbi launch,
+# recorded on the stream the kernel runs on
+LAUNCH_EVENTS: list | None = None
+
 
 def make_gains(h: int, step: float, device="cuda") -> torch.Tensor:
     """2^((g - (2^h - 1)/2) * step) for g < 2^h, float32 (src/tcq_proto.py:247-249).
@@ -53,10 +57,11 @@ def viterbi_ub_cuda(x: torch.Tensor, small: torch.Tensor, K: int, nu: int, m: in
                     gains_hi: torch.Tensor | None = None, mix: int = 0, n_cand: int = 0, return_code: bool = False,
                     tail_biting: bool = False, tb_passes: int = 2, tb_cand1: int = 0, tb_window: int = 0,
                     m_extra: tuple = (), pair_parity=False, _mid: int = 0, _tail: bool = False, _steps: int = 0,
-                    _rot: int = 0):
+                    _rot: int = 0, _raw_code: bool = False):
     """Joint (gain, trellis) Viterbi over tiles x [N, T] on the GPU; see src/tcq_proto.py:567-583 for the meaning
     of every argument. Returns rec [N, T]; or (rec, gain index, level index) with return_code; or (rec, end
-    state) with return_end_state; or (rec, mid state) for an internal first tail-biting pass."""
+    state) with return_end_state; or (rec, mid state) for an internal first tail-biting pass. _raw_code with
+    return_code gives (rec, code) with the kernel's packed int32 code (gain index << 16 | level index)."""
     _lib.require_device(x)
     if tail_biting:
         N, T = x.shape
@@ -81,7 +86,8 @@ def viterbi_ub_cuda(x: torch.Tensor, small: torch.Tensor, K: int, nu: int, m: in
                                          _tail=True, _mid=h, _rot=shift, **common)
             else:  # closed pass writing rec / code back at the original positions
                 out = viterbi_ub_cuda(xf, small, K, nu, m, gains, wts=w_full, n_cand=n_cand, init_state=mid,
-                                      return_code=return_code, _tail=True, _rot=shift, **common)
+                                      return_code=return_code, _tail=True, _rot=shift, _raw_code=_raw_code,
+                                      **common)
         return out
 
     N, ld = x.shape
@@ -116,14 +122,21 @@ def viterbi_ub_cuda(x: torch.Tensor, small: torch.Tensor, K: int, nu: int, m: in
     cand = torch.empty((N, T // sub, G_run), dtype=torch.uint8, device=dev) if G_run < Gfull else None
     me = (list(m_extra) + [0, 0, 0])[:3]
     p = _lib.ptr
+    evs = None
+    if LAUNCH_EVENTS is not None:
+        evs = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        evs[0].record(torch.cuda.current_stream())
     rc = _lib.lib().tcq_viterbi(p(xf), p(w), p(tab), p(g), p(rec), p(bp), p(gsel), p(init), p(end), p(tab_hi), p(g_hi),
                                 p(cand), p(best), p(code), p(mid), _mid, int(_tail), N, T, S, U, G_run, Gfull, m, sub,
                                 tab_hi.numel() // nl, mix if small_hi is not None else 0, me[0], me[1], me[2], nl, ld,
                                 _rot, p(pbits), pp, _lib.stream_ptr())
     if rc != 0:
         raise RuntimeError(f"tcq_viterbi: HIP error code {rc}")
+    if evs is not None:
+        evs[1].record(torch.cuda.current_stream())
+        LAUNCH_EVENTS.append(evs)
     if _mid:
         return rec, mid
     if return_code:
-        return rec, code >> 16, code & 0xFFFF
+        return (rec, code) if _raw_code else (rec, code >> 16, code & 0xFFFF)
     return (rec, end) if return_end_state else rec

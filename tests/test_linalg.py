@@ -1,0 +1,50 @@
+"""Blocked dense linear algebra of the matrix quantizer (ltq_amd.linalg) against float64 LAPACK: the recursive
+Cholesky (src/liqk_v2.py:1079), the recursive triangular inverse that replaces solve_triangular(L, I)
+(src/liqk_v2.py:1081) and the SPD solve of the suh refit (src/liqk_v2.py:1163), at sizes whose recursion
+splits unevenly (not multiples of the leaf)."""
+import pytest
+
+torch = pytest.importorskip("torch")
+
+
+def _spd(n, seed, device="cpu"):
+    g = torch.Generator().manual_seed(seed)
+    X = torch.randn((n // 2, n), generator=g, dtype=torch.float64)
+    return (X.T @ X / n + 0.1 * torch.eye(n, dtype=torch.float64)).float().to(device)
+
+
+def _check(n, leaf, nb, device):
+    from ltq_amd import linalg
+    A = _spd(n, n, device)
+    L, info = linalg.cholesky_lower(A, leaf=leaf)
+    assert int(info) == 0
+    Lr = torch.linalg.cholesky(A.double().cpu())
+    Lc = L.double().cpu()
+    assert torch.equal(Lc, torch.tril(Lc))
+    assert (Lc - Lr).abs().max() <= 2e-6 * Lr.abs().max()
+    Li = linalg.tri_inv_lower(L, leaf=leaf).double().cpu()
+    assert torch.equal(Li, torch.tril(Li))
+    assert (Li @ Lc - torch.eye(n, dtype=torch.float64)).abs().max() <= 1e-5
+    b = torch.randn(n, generator=torch.Generator().manual_seed(1)).to(device)
+    x = linalg.spd_solve(A, b, nb=nb).double().cpu()
+    xr = torch.linalg.solve(A.double().cpu(), b.double().cpu())
+    assert (x - xr).norm() <= 1e-5 * xr.norm()
+
+
+@pytest.mark.parametrize("n,leaf,nb", [(300, 128, 64), (1100, 256, 200), (777, 2048, 512)])
+def test_blocked_linalg_cpu(n, leaf, nb):
+    _check(n, leaf, nb, "cpu")
+
+
+def test_spd_solve_falls_back_to_lu_for_indefinite():
+    from ltq_amd import linalg
+    A = torch.diag(torch.tensor([2.0, -1.0, 3.0]))
+    b = torch.tensor([2.0, 1.0, 3.0])
+    assert torch.allclose(linalg.spd_solve(A, b), torch.tensor([1.0, -1.0, 1.0]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [5000, 2304])
+def test_blocked_linalg_gpu(n):
+    print(f"blocked linalg n={n}", flush=True)
+    _check(n, 2048 if n > 2304 else 512, 512, "cuda")

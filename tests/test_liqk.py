@@ -88,10 +88,19 @@ def test_gpu_ldlq_sub_matches_float64():
         xn = torch.zeros((M // 16, 256), device=DEV)
         rec_d, d_d, Ui_d, U_d = rec.to(DEV), d.to(DEV), Ui.to(DEV), U.to(DEV)  # alive across the call
         print(f"ldlq_sub ib={ib}", flush=True)
+        code = torch.randint(0, 1 << 19, (M // 16, 256), generator=g, dtype=torch.int32)
+        code_d = code.to(DEV)
+        idx = torch.full((M, 512), -1, dtype=torch.int16, device=DEV)
+        gi = torch.full((M, 512), 255, dtype=torch.uint8, device=DEV)
         rc = _lib.lib().ltq_ldlq_sub(wk_d.data_ptr(), 256, rec_d.data_ptr(), d_d.data_ptr(), 1, Ui_d.data_ptr(), 256,
-                                     U_d.data_ptr(), 256, ib, G.data_ptr(), 256, xn.data_ptr(), M, _lib.stream_ptr())
+                                     U_d.data_ptr(), 256, ib, G.data_ptr(), 256, xn.data_ptr(), M, code_d.data_ptr(),
+                                     idx[:, 256:].data_ptr(), 512, gi[:, 256:].data_ptr(), 512, _lib.stream_ptr())
         assert rc == 0
         torch.cuda.synchronize()
+        cv = code.view(M, 16)
+        assert torch.equal(idx.cpu()[:, 256 + s0:256 + s1], (cv & 0xFFFF).to(torch.int16))
+        assert torch.equal(gi.cpu()[:, 256 + s0:256 + s1], (cv >> 16).to(torch.uint8))
+        assert int((idx.cpu() != -1).sum()) == M * 16 and int((gi.cpu() != 255).sum()) <= M * 16
         g_sub = rec.view(M, 16).double()
         err = (wk[:, s0:s1].double() - d.double().unsqueeze(1) * g_sub) @ Ui.double()[s0:s1, s0:s1]
         ref = wk.double().clone()
