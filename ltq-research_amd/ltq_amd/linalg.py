@@ -1,8 +1,10 @@
 """Dense linear algebra of the matrix quantizer, arranged so that almost all flops land in large library GEMMs
 (hipBLASLt / rocBLAS on MI355X) instead of the launch-bound panel kernels of an unblocked factorization.
 
-  cholesky_lower   A = L L^T, recursive 2 x 2 blocking: L11 = chol(A11), L21 = A21 L11^-T (trsm),
-                   L22 = chol(A22 - L21 L21^T); leaves of at most `leaf` rows go to torch.linalg.cholesky_ex.
+  cholesky_lower   A = L L^T. On the device, matrices above `leaf` rows go to MAGMA's blocked hybrid potrf
+                   (torch's magma backend; rocSOLVER's unblocked panels make its potrf launch-bound at these
+                   sizes); otherwise, and where MAGMA is absent, recursive 2 x 2 blocking: L11 = chol(A11),
+                   L21 = A21 L11^-T (trsm), L22 = chol(A22 - L21 L21^T), leaves to torch.linalg.cholesky_ex.
                    Used for src/liqk_v2.py:1079 (the flipped, damped Hessian) and for the SPD system of the
                    suh refit (src/liqk_v2.py:1163).
   tri_inv_lower    L^-1 for lower-triangular L, recursive: [[A, 0], [B, C]]^-1 = [[A^-1, 0], [-C^-1 B A^-1, C^-1]].
@@ -25,21 +27,45 @@ def _split(n: int) -> int:
     return h if h > 0 else n // 2
 
 
-def cholesky_lower(A: torch.Tensor, leaf: int = 2048) -> Tuple[torch.Tensor, torch.Tensor]:
+_MAGMA = [None]
+
+
+def _magma_cholesky(A: torch.Tensor):
+    """torch.linalg.cholesky_ex through the magma backend, or None where the build has no MAGMA."""
+    if _MAGMA[0] is False:
+        return None
+    prev = torch.backends.cuda.preferred_linalg_library()
+    try:
+        torch.backends.cuda.preferred_linalg_library("magma")
+        L, info = torch.linalg.cholesky_ex(A)
+        _MAGMA[0] = True
+        return L, info.to(torch.int64)
+    except RuntimeError:
+        _MAGMA[0] = False
+        return None
+    finally:
+        torch.backends.cuda.preferred_linalg_library(prev)
+
+
+def cholesky_lower(A: torch.Tensor, leaf: int = 2048, magma: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
     """(L, info): lower Cholesky factor of symmetric A (only its lower triangle is read) and an int tensor that is
-    0 when every leaf factorization succeeded."""
+    0 when the factorization succeeded."""
     n = A.shape[0]
+    if magma and A.is_cuda and n > leaf:
+        r = _magma_cholesky(A)
+        if r is not None:
+            return r
     if n <= leaf:
         L, info = torch.linalg.cholesky_ex(A)
         return L, info.to(torch.int64)
     h = _split(n)
     L = torch.zeros_like(A)
-    L11, i1 = cholesky_lower(A[:h, :h], leaf)
+    L11, i1 = cholesky_lower(A[:h, :h], leaf, False)
     L[:h, :h] = L11
     L21 = torch.linalg.solve_triangular(L11.T, A[h:, :h], upper=True, left=False)
     L[h:, :h] = L21
     S = torch.addmm(A[h:, h:], L21, L21.T, alpha=-1.0)
-    L22, i2 = cholesky_lower(S, leaf)
+    L22, i2 = cholesky_lower(S, leaf, False)
     L[h:, h:] = L22
     return L, i1.abs() + i2.abs()
 

@@ -13,9 +13,12 @@ import torch
 
 from . import _lib
 
-# timing hook (off by default): a list receives one (start, end) torch.cuda.Event pair per tcq_viterbi launch,
-# recorded on the stream the kernel runs on
+# timing hook (off by default): a list receives (start, end) torch.cuda.Event pairs around tcq_viterbi launches,
+# recorded on the stream the kernel runs on, for launch pairs 0, LAUNCH_SAMPLE, 2 LAUNCH_SAMPLE, ... counted
+# from the last reset of _launch_count (a tail-biting call issues its two passes as one pair)
 LAUNCH_EVENTS: list | None = None
+LAUNCH_SAMPLE = 1
+_launch_count = 0
 
 
 def make_gains(h: int, step: float, device="cuda") -> torch.Tensor:
@@ -124,8 +127,11 @@ def viterbi_ub_cuda(x: torch.Tensor, small: torch.Tensor, K: int, nu: int, m: in
     p = _lib.ptr
     evs = None
     if LAUNCH_EVENTS is not None:
-        evs = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-        evs[0].record(torch.cuda.current_stream())
+        global _launch_count
+        if (_launch_count // 2) % LAUNCH_SAMPLE == 0:
+            evs = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            evs[0].record(torch.cuda.current_stream())
+        _launch_count += 1
     rc = _lib.lib().tcq_viterbi(p(xf), p(w), p(tab), p(g), p(rec), p(bp), p(gsel), p(init), p(end), p(tab_hi), p(g_hi),
                                 p(cand), p(best), p(code), p(mid), _mid, int(_tail), N, T, S, U, G_run, Gfull, m, sub,
                                 tab_hi.numel() // nl, mix if small_hi is not None else 0, me[0], me[1], me[2], nl, ld,
