@@ -53,6 +53,17 @@ long ltq_slice_bytes(int R, int K, int fmt_K, int frac, int h, int sub);
 int ltq_pack_slice(const int16_t* idx, long ld_idx, const uint8_t* gi, long ld_gi, int R, int K, int fmt_K, int frac,
                    int h, int sub, uint8_t* out, long out_bytes, void* stream);
 
+/* Bytes of one packed row ring of L positions (src/ltq_format.py:48-50, `tile_bytes(L)`, the ring's fp16 scale
+ * excluded). L % 16 == 0, L <= 512, L % sub == 0; -1 otherwise. Host-only arithmetic. */
+long ltq_ring_bytes(int L, int fmt_K, int frac, int h, int sub);
+
+/* Packs n_rings rings of L positions, codes idx [n_rings, L] (int16 label * U + u, row stride ld_idx) and gain
+ * indices gi (uint8, row stride ld_gi), into consecutive records of ltq_ring_bytes(...) bytes, each the fields
+ * codes / planes / lsb / gains of src/ltq_format.py:104-124 (`pack_tile` with L instead of 256) back to back.
+ * Serves the ring tables of src/ple_quant.py:36-67. */
+int ltq_pack_rings(const int16_t* idx, long ld_idx, const uint8_t* gi, long ld_gi, long n_rings, int L, int fmt_K,
+                   int frac, int h, int sub, uint8_t* out, long out_bytes, void* stream);
+
 /* Row scale of a rotated weight matrix w [M, K] (K % 256 == 0, row stride ldw, 16-byte aligned):
  * rms of every 256-column block (clamped at 1e-10, times scale), d_row[M] = fp16-rounded geometric mean of
  * the row's block rms (clamped at 1e-8), e[M, K/256] (int8, row stride lde) = clamp(round(log2(rms / d_row)

@@ -10,6 +10,10 @@
 // 16 kb + c. One wavefront packs one tile: it stages the tile's 256 codes in LDS, then each lane assembles
 // whole 16-bit words.
 //
+// Row rings (src/ltq_format.py:42-50, 104-124 with L instead of 256; the ring tables of src/ple_quant.py): a
+// ring of L positions (L % 16 == 0, L <= 512) packs into one record of the same four fields back to back,
+// 2 (L/16 + L/16 (K-2) + lsb words + gain words) bytes; rings are consecutive records.
+//
 // Roofline: HBM, 3 bytes in per weight (int16 code + uint8 gain index) plus the tile bytes out.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -19,30 +23,40 @@
 namespace {
 
 constexpr int kWaves = 4;
+constexpr int kMaxL = 512;
 
+// Field sizes of one tile / ring of L positions (src/ltq_format.py:42-50): u16 words per field and where each
+// field starts -- region offsets of a slice (structure of arrays) or word offsets inside a ring record.
 struct PackGeo {
-    int K, frac, h, sub, U;
-    int n[4];      // u16 words per tile of each region
-    long off[4];   // byte offset of each region
-    long total;    // bytes of the slice
+    int K, frac, h, sub, U, L;
+    int n[4];      // u16 words per tile / ring: codes, planes, lsb, gains
+    long off[4];   // slice: byte offset of each region; rings: word offset of each field inside a record
+    long total;    // slice: bytes of the slice; rings: bytes of one record
 };
 
 __host__ __device__ inline long align64(long v) { return (v + 63) & ~63L; }
 
-__host__ __device__ inline PackGeo pack_geo(int R, int Kc, int K, int frac, int h, int sub)
+__host__ __device__ inline int lsb_bits(int frac, int L) { return frac == 0 ? L : frac == 1 ? L / 2 : 3 * L / 4; }
+
+__host__ __device__ inline void field_words(PackGeo& g, int K, int frac, int h, int sub, int L)
 {
-    PackGeo g;
     g.K = K;
     g.frac = frac;
     g.h = h;
     g.sub = sub;
     g.U = 1 << (K - 1);
+    g.L = L;
+    g.n[0] = L / 16;
+    g.n[1] = L / 16 * (K > 2 ? K - 2 : 0);
+    g.n[2] = K > 1 ? (lsb_bits(frac, L) + 15) / 16 : 0;
+    g.n[3] = h ? (L / sub * h + 15) / 16 : 0;
+}
+
+__host__ __device__ inline PackGeo pack_geo(int R, int Kc, int K, int frac, int h, int sub)
+{
+    PackGeo g;
+    field_words(g, K, frac, h, sub, 256);
     const long T = (long)(R / 16) * (Kc / 16);
-    const int lsb_bits = frac == 0 ? 256 : frac == 1 ? 128 : 192;
-    g.n[0] = 16;
-    g.n[1] = 16 * (K > 2 ? K - 2 : 0);
-    g.n[2] = K > 1 ? (lsb_bits + 15) / 16 : 0;
-    g.n[3] = h ? (256 / sub * h + 15) / 16 : 0;
     long o = 0;
     for (int r = 0; r < 4; r++) {
         o = align64(o);
@@ -51,6 +65,66 @@ __host__ __device__ inline PackGeo pack_geo(int R, int Kc, int K, int frac, int 
     }
     g.total = o;
     return g;
+}
+
+__host__ __device__ inline PackGeo ring_geo(int L, int K, int frac, int h, int sub)
+{
+    PackGeo g;
+    field_words(g, K, frac, h, sub, L);
+    long o = 0;
+    for (int r = 0; r < 4; r++) {
+        g.off[r] = o;
+        o += g.n[r];
+    }
+    g.total = 2 * o;
+    return g;
+}
+
+__device__ inline void wave_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Word wr of field reg of one tile / ring whose codes and gain indices sit in LDS (position t = 0 .. L-1):
+//   codes  bit j of word w = label & 1 at position 16 w + j
+//   planes plane p = 1 .. K-2 of u, L/16 words each, same layout
+//   lsb    lowest bit of u: every position / one per pair (D2) / the first three of each quad (D4)
+//   gains  gain index of each sub-block, h bits LSB first, back to back
+__device__ inline uint32_t field_word(const int16_t* ix, const uint8_t* gs, const PackGeo& g, int reg, int wr)
+{
+    const int W = g.L / 16;
+    uint32_t word = 0;
+    for (int j = 0; j < 16; j++) {
+        const int i = 16 * wr + j;  // bit index within the field's stream
+        uint32_t bit = 0;
+        if (reg == 0) {
+            bit = ((uint32_t)ix[i] >> (g.K - 1)) & 1;
+        } else if (reg == 1) {
+            const int p = 1 + wr / W, t = 16 * (wr % W) + j;
+            bit = (((uint32_t)ix[t] & (g.U - 1)) >> p) & 1;
+        } else if (reg == 2) {
+            if (i < lsb_bits(g.frac, g.L)) {
+                const int t = g.frac == 0 ? i : g.frac == 1 ? 2 * i : 4 * (i / 3) + i % 3;
+                bit = (uint32_t)ix[t] & 1;
+            }
+        } else {
+            if (i < g.L / g.sub * g.h) bit = ((uint32_t)gs[g.sub * (i / g.h)] >> (i % g.h)) & 1;
+        }
+        word |= bit << j;
+    }
+    return word;
+}
+
+__device__ inline void word_region(const PackGeo& g, int w, int& reg, int& wr)
+{
+    reg = 0;
+    wr = w;
+    while (wr >= g.n[reg]) {
+        wr -= g.n[reg];
+        reg++;
+    }
 }
 
 __global__ __launch_bounds__(64 * kWaves) void pack_kernel(const int16_t* __restrict__ idx, long ld_idx,
@@ -78,52 +152,52 @@ __global__ __launch_bounds__(64 * kWaves) void pack_kernel(const int16_t* __rest
             s_ix[wv][t] = idx[row * ld_idx + col];
             s_g[wv][t] = gi[row * ld_gi + col];
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        wave_sync();
         const int W = g.n[0] + g.n[1] + g.n[2] + g.n[3];
         for (int w = lane; w < W; w += 64) {
-            int reg = 0, wr = w;
-            while (wr >= g.n[reg]) {
-                wr -= g.n[reg];
-                reg++;
-            }
-            uint32_t word = 0;
-            for (int j = 0; j < 16; j++) {
-                const int i = 16 * wr + j;  // bit index within the region's stream of this tile
-                uint32_t bit = 0;
-                if (reg == 0) {
-                    bit = ((uint32_t)s_ix[wv][i] >> (g.K - 1)) & 1;  // label & 1
-                } else if (reg == 1) {
-                    const int p = 1 + wr / 16, t = 16 * (wr % 16) + j;
-                    bit = (((uint32_t)s_ix[wv][t] & (g.U - 1)) >> p) & 1;
-                } else if (reg == 2) {
-                    const int nb = g.frac == 0 ? 256 : g.frac == 1 ? 128 : 192;
-                    if (i < nb) {
-                        const int t = g.frac == 0 ? i : g.frac == 1 ? 2 * i : 4 * (i / 3) + i % 3;
-                        bit = (uint32_t)s_ix[wv][t] & 1;
-                    }
-                } else {
-                    const int nb = 256 / g.sub * g.h;
-                    if (i < nb) bit = ((uint32_t)s_g[wv][g.sub * (i / g.h)] >> (i % g.h)) & 1;
-                }
-                word |= bit << j;
-            }
-            *(uint16_t*)(out + g.off[reg] + 2 * (tile * g.n[reg] + wr)) = (uint16_t)word;
+            int reg, wr;
+            word_region(g, w, reg, wr);
+            *(uint16_t*)(out + g.off[reg] + 2 * (tile * g.n[reg] + wr)) = (uint16_t)field_word(s_ix[wv], s_g[wv], g, reg, wr);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        wave_sync();
     }
+}
+
+// one wavefront per ring: record i = fields codes, planes, lsb, gains back to back (g.total bytes)
+__global__ __launch_bounds__(64 * kWaves) void pack_rings_kernel(const int16_t* __restrict__ idx, long ld_idx,
+                                                                 const uint8_t* __restrict__ gi, long ld_gi, long n,
+                                                                 PackGeo g, uint8_t* __restrict__ out)
+{
+    __shared__ int16_t s_ix[kWaves][kMaxL];
+    __shared__ uint8_t s_g[kWaves][kMaxL];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int W = g.n[0] + g.n[1] + g.n[2] + g.n[3];
+    for (long ring = (long)blockIdx.x * kWaves + wv; ring < n; ring += (long)gridDim.x * kWaves) {
+        for (int t = lane; t < g.L; t += 64) {
+            s_ix[wv][t] = idx[ring * ld_idx + t];
+            s_g[wv][t] = gi[ring * ld_gi + t];
+        }
+        wave_sync();
+        uint16_t* rec = (uint16_t*)(out + ring * g.total);
+        for (int w = lane; w < W; w += 64) {
+            int reg, wr;
+            word_region(g, w, reg, wr);
+            rec[g.off[reg] + wr] = (uint16_t)field_word(s_ix[wv], s_g[wv], g, reg, wr);
+        }
+        wave_sync();
+    }
+}
+
+bool fmt_ok(int fmt_K, int frac, int h, int sub)
+{
+    return fmt_K >= 1 && fmt_K <= 8 && frac >= 0 && frac <= 2 && h >= 0 && h <= 8 && sub > 0;
 }
 
 }  // namespace
 
 extern "C" long ltq_slice_bytes(int R, int K, int fmt_K, int frac, int h, int sub)
 {
-    if (R < 0 || K < 0 || R % 16 || K % 16 || fmt_K < 1 || fmt_K > 8 || frac < 0 || frac > 2 || h < 0 || h > 8 || sub <= 0 ||
-        256 % sub)
-        return -1;
+    if (R < 0 || K < 0 || R % 16 || K % 16 || !fmt_ok(fmt_K, frac, h, sub) || 256 % sub) return -1;
     return pack_geo(R, K, fmt_K, frac, h, sub).total;
 }
 
@@ -140,5 +214,26 @@ extern "C" int ltq_pack_slice(const int16_t* idx, long ld_idx, const uint8_t* gi
     if (grid > 65536) grid = 65536;
     hipLaunchKernelGGL(pack_kernel, dim3((unsigned)grid), dim3(64 * kWaves), 0, (hipStream_t)stream, idx, ld_idx, gi, ld_gi,
                        R, K, g, out);
+    return (int)hipGetLastError();
+}
+
+extern "C" long ltq_ring_bytes(int L, int fmt_K, int frac, int h, int sub)
+{
+    if (L <= 0 || L > kMaxL || L % 16 || !fmt_ok(fmt_K, frac, h, sub) || L % sub) return -1;
+    return ring_geo(L, fmt_K, frac, h, sub).total;
+}
+
+extern "C" int ltq_pack_rings(const int16_t* idx, long ld_idx, const uint8_t* gi, long ld_gi, long n_rings, int L,
+                              int fmt_K, int frac, int h, int sub, uint8_t* out, long out_bytes, void* stream)
+{
+    const long rb = ltq_ring_bytes(L, fmt_K, frac, h, sub);
+    if (rb < 0 || n_rings < 0 || ld_idx < L || ld_gi < L || out_bytes < rb * n_rings) return -1;
+    if (n_rings == 0) return 0;
+    if (!idx || !gi || !out) return -1;
+    const PackGeo g = ring_geo(L, fmt_K, frac, h, sub);
+    long grid = (n_rings + kWaves - 1) / kWaves;
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL(pack_rings_kernel, dim3((unsigned)grid), dim3(64 * kWaves), 0, (hipStream_t)stream, idx, ld_idx, gi,
+                       ld_gi, n_rings, g, out);
     return (int)hipGetLastError();
 }
