@@ -27,6 +27,14 @@ int tcq_viterbi(const float* x, const float* w, const float* tab, const float* g
                 int G, int Gfull, int m, int sub, int U_hi, int mix, int m2, int m3, int m4, int nl, int ld, int rot,
                 uint32_t* pbits, int pp, void* stream);
 
+/* LUT sub-block quantization of the diagonal profile: for S sub-blocks of 16 weights xs[S, 16] with weights
+ * dh[S, 16], bucket b = clamp(rint(x * inv_step + half_b), 0, nb - 1) picks a row of 64 candidates of lut[nb, 64];
+ * the first candidate with the lowest sum_j dh (xs - lut[b_j][c])^2 gives out[S, 16] = lut[b_j][c]. Same
+ * signature, argument meaning and results as src/cuda/tcq_viterbi.cu:806-811 (bound at src/tcq_proto.py:530-532),
+ * with the rounding of nvcc's default contraction written out (fma for the bucket argument and the sums). */
+int lut_subs_quant(const float* xs, const float* dh, const float* lut, float* out, int S, float inv_step, float half_b,
+                   int nb, void* stream);
+
 /* Normalized block FWHT-256 along rows: y[r, :] = FWHT256 of (x[r, :] op s), fp32 out.
  * Replaces the torch function src/iqk_format.py:153-170 (`fwht_inplace`) as called with a fused scale at
  * src/liqk_v2.py:438-439 (smode 1: x / s[col], smode 2: x * s[col], 0: none).

@@ -39,11 +39,12 @@ def lut_subs_quant_cuda(x_subs: torch.Tensor, dh: torch.Tensor, lut_val: torch.T
     _lib.require_device(x_subs)
     x = x_subs.float().contiguous()
     d = dh.float().reshape(x.shape).contiguous()
+    t = lut_val.float().contiguous()
     out = torch.empty_like(x)
-    rc = _lib.lib().lut_subs_quant(x.data_ptr(), d.data_ptr(), lut_val.float().contiguous().data_ptr(), out.data_ptr(),
-                                   x.shape[0], inv_step, half_b, lut_val.shape[0], _lib.stream_ptr())
+    rc = _lib.lib().lut_subs_quant(x.data_ptr(), d.data_ptr(), t.data_ptr(), out.data_ptr(), x.shape[0], inv_step,
+                                   half_b, t.shape[0], _lib.stream_ptr())
     if rc != 0:
-        raise RuntimeError(f"lut_subs_quant: HIP error code {rc}")
+        raise RuntimeError(f"lut_subs_quant: HIP error code {rc}" if rc > 0 else "lut_subs_quant: rejected arguments")
     return out
 
 

@@ -487,3 +487,44 @@ void ltq_oracle_fwht256(float* x, long n_blocks)
         for (int i = 0; i < 256; i++) y[i] = y[i] * 0.0625f;
     }
 }
+
+/* lut_subs_kernel (tcq_viterbi.cu:771-800): per sub-block of 16 weights, bucket b_j = clamp(rint(x_j inv_step +
+ * half_b), 0, nb - 1), err_c = sum_j d_j (x_j - lut[b_j][c])^2 over 64 candidates in order j = 0..15, the first
+ * minimal c wins (strict '<' scan), out_j = lut[b_j][c]. The products and sums are written with fmaf as nvcc's
+ * default contraction (--fmad=true) forms them: fma(x, inv_step, half_b) and err = fma(d e, e, err). A NaN
+ * bucket argument gives bucket 0, as the device's float-to-int conversion does. */
+static int lut_bucket(float x, float inv_step, float half_b, int nb)
+{
+    const float r = rintf(fmaf(x, inv_step, half_b));
+    if (r != r) return 0;
+    if (r < 0.f) return 0;
+    if (r > (float)(nb - 1)) return nb - 1;
+    return (int)r;
+}
+
+void ltq_oracle_lut_subs(const float* xs, const float* dh, const float* lut, float* out, long S, float inv_step,
+                         float half_b, int nb)
+{
+#pragma omp parallel for schedule(static)
+    for (long i = 0; i < S; i++) {
+        float err[64];
+        int b[16];
+        for (int c = 0; c < 64; c++) err[c] = 0.f;
+        for (int j = 0; j < 16; j++) {
+            const float x = xs[i * 16 + j], d = dh[i * 16 + j];
+            b[j] = lut_bucket(x, inv_step, half_b, nb);
+            for (int c = 0; c < 64; c++) {
+                const float e = x - lut[(long)b[j] * 64 + c];
+                err[c] = fmaf(d * e, e, err[c]);
+            }
+        }
+        int best = 0;
+        float be = err[0];
+        for (int c = 1; c < 64; c++)
+            if (err[c] < be) {
+                be = err[c];
+                best = c;
+            }
+        for (int j = 0; j < 16; j++) out[i * 16 + j] = lut[(long)b[j] * 64 + best];
+    }
+}

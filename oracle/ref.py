@@ -42,6 +42,8 @@ def lib():
         L.ltq_oracle_tcq_viterbi.argtypes = [vp] * 13 + [ci] * 19 + [vp, ci]
         L.ltq_oracle_fwht256.restype = None
         L.ltq_oracle_fwht256.argtypes = [vp, ctypes.c_long]
+        L.ltq_oracle_lut_subs.restype = None
+        L.ltq_oracle_lut_subs.argtypes = [vp] * 4 + [ctypes.c_long, ctypes.c_float, ctypes.c_float, ci]
         L.ltq_oracle_labels.restype = None
         L.ltq_oracle_labels.argtypes = [ci] * 6 + [vp]
         L.ltq_brute_force.restype = ctypes.c_double
@@ -169,6 +171,17 @@ def fwht256_ref(x) -> np.ndarray:
     assert a.shape[-1] % 256 == 0
     lib().ltq_oracle_fwht256(_p(a), a.size // 256)
     return a
+
+
+def lut_subs_ref(xs, dh, lut, inv_step: float, half_b: float) -> np.ndarray:
+    """The reference's lut_subs_quant (tcq_viterbi.cu:768-811) over the oracle: xs, dh [S, 16], lut [nb, 64]."""
+    x = np.ascontiguousarray(xs, np.float32).reshape(-1, 16)
+    d = np.ascontiguousarray(dh, np.float32).reshape(x.shape)
+    t = np.ascontiguousarray(lut, np.float32)
+    assert t.shape[1] == 64
+    out = np.empty_like(x)
+    lib().ltq_oracle_lut_subs(_p(x), _p(d), _p(t), _p(out), x.shape[0], inv_step, half_b, t.shape[0])
+    return out
 
 
 def labels_ref(S=1024, m=359, m_extra=()) -> np.ndarray:
