@@ -34,6 +34,8 @@ struct GpuX {
     __device__ __forceinline__ float fmin(float x, float y) const { return __builtin_fminf(x, y); }
     __device__ __forceinline__ float shfl_xor(float v, int m) const { return __shfl_xor(v, m, 64); }
     __device__ __forceinline__ int shfl_xor(int v, int m) const { return __shfl_xor(v, m, 64); }
+    // a value every lane holds equally, pinned to a scalar register
+    __device__ __forceinline__ int uni(int v) const { return __builtin_amdgcn_readfirstlane(v); }
     // lane l's value (l uniform), into a scalar register
     __device__ __forceinline__ uint32_t readlane(uint32_t v, int l) const
     {

@@ -59,6 +59,7 @@ struct CpuX {
         return r;
     }
     int shfl_xor(int v, int m) const { return (int)xor_lane((uint32_t)v, m); }
+    int uni(int v) const { return v; }
     uint32_t readlane(uint32_t v, int l) const
     {
         const int w = tid_ >> 6;
