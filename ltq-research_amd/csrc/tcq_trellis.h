@@ -731,26 +731,30 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
         X_.lds_sync();
     }
     const int bi_all = (int)X_.readlane((uint32_t)s_ctl[0], 0);  // uniform: scalar registers
-    // The traceback and the reconstruction run on wavefront 0 alone: the other wavefronts are done (no
-    // barrier follows), and wavefront 0 issues every decision-word copy itself, so that its own vmcnt
-    // tracks them.
-    if (wv != 0) return;
 
     // ---- traceback (tcq_viterbi.cu:601-661) ----------------------------------------------------------
     // One LDS lookup per phase: the phase's output state names the (wave, lane) that computed it and the
     // block; that lane's decision bits give the phase's input state, the intermediate state and the parity
-    // classes. Lanes 0-3 fetch the four possible next lookups one phase ahead; v_readlane picks the true one.
+    // classes. Lanes of the walking wavefront fetch the possible next lookups one phase ahead; v_readlane
+    // picks the true one.
     uint32_t* s_rec = (uint32_t*)s_st;  // per phase: output state | slot << 10 | e << 14 | classes << 15
-    bool walked = false;
+    // Streamlined walk (whole chunks, one block per lane, a second wavefront, a ring of at least 3 chunks;
+    // every matrix-path tile): wavefront 0 walks, wavefront 1 copies the decision words of the chunks ahead
+    // global -> LDS, one barrier per chunk hands them over, and every thread writes the outputs. Otherwise
+    // wavefront 0 alone walks (copying its own words) and writes the outputs, and the others are done.
+    bool fast = false;
+    if constexpr (RB == 2) fast = T % CK == 0 && nthr >= 128 && SM.nslot >= 3;
+    if (!fast && wv != 0) return;
+    int out_t0 = lane, out_dt = 64;
     if constexpr (RB == 2) {
-        // Streamlined walk for whole chunks (T % CK == 0; every matrix-path tile): no per-phase control flow but
-        // one uniform stop check. Bit positions are compile-time (one block per lane); at the start of each
-        // phase, lane L + 4 gp fetches the decision words of the phase below for the input-state hypothesis L
-        // (the phase's two decision bits h e) and, when the phase starts a sub-block, for every gain slot gp
-        // the merge may choose, together with the merge choice of hypothesis L, so neither the next chunk nor a
-        // slot change ever waits on an LDS round trip.
-        if (T % CK == 0) {
-            walked = true;
+        // No per-phase control flow but one uniform stop check. Bit positions are compile-time (one block per
+        // lane); at the start of each phase, lane L + 4 gp fetches the decision words of the phase below for
+        // the input-state hypothesis L (the phase's two decision bits h e) and, when the phase starts a
+        // sub-block, for every gain slot gp the merge may choose, together with the merge choice of hypothesis
+        // L, so neither the next chunk nor a slot change ever waits on an LDS round trip.
+        if (fast) {
+            out_t0 = tid;
+            out_dt = nthr;
             uint32_t* ring = (uint32_t*)(sm + SM.ring);
             const int nslot = SM.nslot, slot_words = SM.slot_words;
             const int nloads = (G * Q * 16 * NW + 63) / 64;  // wave loads per chunk
@@ -775,15 +779,23 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
                 }
             };
             auto min_i = [](int x, int y) { return x < y ? x : y; };
-            for (int j = 0; j < nslot - 1 && nchunk - 1 - j >= 0; j++) issue(nchunk - 1 - j);
-            X_.wait_loads(min_i(nslot - 2, nchunk - 1) * nloads);  // the last chunk has landed
+            auto max_i = [](int x, int y) { return x > y ? x : y; };
+            auto count = [](int lo, int hi) { return hi >= lo ? hi - lo + 1 : 0; };
+            const int mid_ph = a.mid_st ? (a.mid_t - 1) >> 1 : -1;
+            const int kmax = a.mid_st ? nchunk - mid_ph / NPC : nchunk;  // chunks walked
+            // copier: chunks nchunk-1 .. nchunk-nslot+1 now; before the first barrier the two the walk reads
+            // first (its chunk and, from its last phase on, the one below) have landed
+            if (wv == 1) {
+                for (int j = 0; j < nslot - 1 && nchunk - 1 - j >= 0; j++) issue(nchunk - 1 - j);
+                X_.wait_loads(count(max_i(0, nchunk - nslot + 1), nchunk - 3) * nloads);
+            }
+            X_.lds_sync();
             // per-lane hypothesis: L = lane & 3 (input-state bits h e), gp = lane >> 2 (gain slot at a boundary)
             const int hypL = lane & 3;
             const int gp = min_i(lane >> 2, G - 1);
             const int sxL = GE::start(hypL, 0, 0);
             const int wL = (sxL >> 8) & (Q - 1), lL = (sxL >> 2) & 63;
             int st = bi_all % S, gs = bi_all / S, cstar = 0;
-            const int mid_ph = a.mid_st ? (a.mid_t - 1) >> 1 : -1;
             int nbnd = ((T - 1) / sub) * sub, jb = (T - 1) / sub;
             uint32_t c0, c1, gv = 0;
             {  // exact words of the walk's first phase, in every lane
@@ -795,107 +807,113 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
             }
             int sel = 0, mid_val = 0;
             bool stop = false;
-            for (int cc = nchunk - 1; cc >= 0 && !stop; cc--) {
-                if (cc - nslot + 1 >= 0) issue(cc - nslot + 1);
-                const uint32_t* slot = ring + (cc % nslot) * slot_words;
-                const uint32_t* slot_next = ring + ((cc + nslot - 1) % nslot) * slot_words;  // chunk cc - 1
-                static_for<0, NPC>([&](auto Kc) {
-                    constexpr int pi = NPC - 1 - decltype(Kc)::value;
-                    constexpr int PT = MM::PT(pi);
-                    constexpr int P = MM::OFF(pi);
-                    constexpr int o = P - 32 * (P >> 5);
-                    constexpr int NB_ = MM::PBLK(PT);  // the phase's decision bits, first push highest
-                    constexpr bool TWO_WORDS = o + NB_ > 32;
-                    if (stop) return;
-                    const int ta = cc * CK + 2 * pi, ph = ta >> 1;
-                    const uint32_t W0 = X_.readlane(c0, sel);
-                    const uint32_t W1 = TWO_WORDS ? X_.readlane(c1, sel) : 0u;
-                    const bool bnd = G > 1 && ta == nbnd && ta > 0;
-                    const int qq = (st >> 8) & (Q - 1), ll = (st >> 2) & 63, jo = st & 3;
-                    // prefetch the words of the phase below for every hypothesis (and slot at a boundary), and
-                    // the merge choice of every hypothesis (an in-bounds byte even where it is not used)
-                    if (pi > 0 || cc > 0) {
-                        constexpr int PN = pi > 0 ? pi - 1 : NPC - 1;
-                        constexpr int PNw = MM::OFF(PN) >> 5;
-                        if (pi == 0) X_.wait_loads(min_i(nslot - 2, cc - 1) * nloads);  // chunk cc - 1 has landed
-                        const int su = GE::start(0, qq, ll);
-                        const int gsl = bnd ? gp : gs;
-                        const int wi = ((gsl * Q + (((su >> 8) & (Q - 1)) | wL)) * NW + PNw) * 64 + (((su >> 2) & 63) | lL);
-                        const uint32_t* tsl = pi > 0 ? slot : slot_next;
-                        c0 = tsl[wi];
-                        c1 = tsl[wi + 64];
-                        gv = s_gsel[G > 1 ? jb * S + (su | sxL) : 0];
-                    }
-                    const uint32_t F = TWO_WORDS ? (uint32_t)(((((uint64_t)W0 << 32) | W1) >> (64 - o - NB_)) & ((1u << NB_) - 1u))
-                                                 : (W0 >> (32 - o - NB_)) & ((1u << NB_) - 1u);
-                    // n bits of F from position k on; the shift NB_ - k - n comes from tables indexed by jo
-                    auto fld = [&](int sh, int nbit) -> int { return (int)((F >> sh) & ((1u << nbit) - 1u)); };
-                    auto tab8 = [](uint32_t t, int i) -> int { return (int)((t >> (8 * i)) & 0xFFu); };
-                    int h = 0, e = 0, pa = 0, pb = 0;
-                    if constexpr (MD == 0) {  // e at 2 + ca, h at e
-                        e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 4) << 16) | ((NB_ - 4) << 24), jo), 1);
-                        h = fld(NB_ - 1 - e, 1);
-                    } else if constexpr (MD == 1) {  // p at 4 + 4 ca + cb, e at 2 + 4 ca + p, h at e
-                        const int p = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 6) << 8) | ((NB_ - 9) << 16) | ((NB_ - 10) << 24), jo), 1);
-                        e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 7) << 16) | ((NB_ - 7) << 24), jo) - p, 1);
-                        h = fld(NB_ - 1 - e, 1);
-                        pa = pb = p;
-                    } else if constexpr (!EQ) {
-                        if constexpr (PT == 1) {  // v3 at 8 + 10 ca + 3 cb (3 bits); e at 4 + 10 ca + idx; h at 2 e + c
-                            const int v3 = fld(tab8(((NB_ - 11) << 0) | ((NB_ - 14) << 8) | ((NB_ - 21) << 16) | ((NB_ - 24) << 24), jo), 3);
-                            const int idx = (0xEDEC >> (2 * v3)) & 3;
-                            cstar = idx >> 1;
-                            const int bsel = idx & 1;
-                            e = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 5) << 8) | ((NB_ - 15) << 16) | ((NB_ - 15) << 24), jo) - idx, 1);
-                            h = fld(NB_ - 1 - 2 * e - cstar, 1);
-                            pb = bsel ^ cstar;
-                            pa = bsel;
-                        } else {  // bsel at 4 + 6 ca + 2 cb + c; e at 2 + 6 ca + bsel; h at e
-                            const int bsel = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 7) << 8) | ((NB_ - 11) << 16) | ((NB_ - 13) << 24), jo) - cstar, 1);
-                            e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 9) << 16) | ((NB_ - 9) << 24), jo) - bsel, 1);
-                            h = fld(NB_ - 1 - e, 1);
-                            pb = bsel ^ cstar;
-                            pa = bsel;
+            for (int k = 0; k < kmax; k++) {
+                const int cc = nchunk - 1 - k;
+                if (wv == 1) {  // chunk cc - nslot + 1 into the slot chunk cc + 1 left; chunk cc - 2 lands first
+                    if (cc - nslot + 1 >= 0) issue(cc - nslot + 1);
+                    X_.wait_loads(count(max_i(0, cc - nslot + 1), cc - 3) * nloads);
+                }
+                if (wv == 0) {
+                    const uint32_t* slot = ring + (cc % nslot) * slot_words;
+                    const uint32_t* slot_next = ring + ((cc + nslot - 1) % nslot) * slot_words;  // chunk cc - 1
+                    static_for<0, NPC>([&](auto Kc) {
+                        constexpr int pi = NPC - 1 - decltype(Kc)::value;
+                        constexpr int PT = MM::PT(pi);
+                        constexpr int P = MM::OFF(pi);
+                        constexpr int o = P - 32 * (P >> 5);
+                        constexpr int NB_ = MM::PBLK(PT);  // the phase's decision bits, first push highest
+                        constexpr bool TWO_WORDS = o + NB_ > 32;
+                        if (stop) return;
+                        const int ta = cc * CK + 2 * pi, ph = ta >> 1;
+                        const uint32_t W0 = X_.readlane(c0, sel);
+                        const uint32_t W1 = TWO_WORDS ? X_.readlane(c1, sel) : 0u;
+                        const bool bnd = G > 1 && ta == nbnd && ta > 0;
+                        const int qq = (st >> 8) & (Q - 1), ll = (st >> 2) & 63, jo = st & 3;
+                        // prefetch the words of the phase below for every hypothesis (and slot at a boundary), and
+                        // the merge choice of every hypothesis (an in-bounds byte even where it is not used)
+                        if (pi > 0 || cc > 0) {
+                            constexpr int PN = pi > 0 ? pi - 1 : NPC - 1;
+                            constexpr int PNw = MM::OFF(PN) >> 5;
+                            const int su = GE::start(0, qq, ll);
+                            const int gsl = bnd ? gp : gs;
+                            const int wi = ((gsl * Q + (((su >> 8) & (Q - 1)) | wL)) * NW + PNw) * 64 + (((su >> 2) & 63) | lL);
+                            const uint32_t* tsl = pi > 0 ? slot : slot_next;
+                            c0 = tsl[wi];
+                            c1 = tsl[wi + 64];
+                            gv = s_gsel[G > 1 ? jb * S + (su | sxL) : 0];
                         }
-                    } else {
-                        if constexpr (PT == 1) {  // c at 6 + 4 ca + cb; e at 4 + 4 ca + c; h at 2 e + c
-                            cstar = fld(tab8(((NB_ - 7) << 0) | ((NB_ - 8) << 8) | ((NB_ - 11) << 16) | ((NB_ - 12) << 24), jo), 1);
-                            e = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 5) << 8) | ((NB_ - 9) << 16) | ((NB_ - 9) << 24), jo) - cstar, 1);
-                            h = fld(NB_ - 1 - 2 * e - cstar, 1);
-                        } else {  // e at 2 + 2 ca + c; h at e
-                            e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 5) << 16) | ((NB_ - 5) << 24), jo) - cstar, 1);
+                        const uint32_t F = TWO_WORDS ? (uint32_t)(((((uint64_t)W0 << 32) | W1) >> (64 - o - NB_)) & ((1u << NB_) - 1u))
+                                                     : (W0 >> (32 - o - NB_)) & ((1u << NB_) - 1u);
+                        // n bits of F from position k on; the shift NB_ - k - n comes from tables indexed by jo
+                        auto fld = [&](int sh, int nbit) -> int { return (int)((F >> sh) & ((1u << nbit) - 1u)); };
+                        auto tab8 = [](uint32_t t, int i) -> int { return (int)((t >> (8 * i)) & 0xFFu); };
+                        int h = 0, e = 0, pa = 0, pb = 0;
+                        if constexpr (MD == 0) {  // e at 2 + ca, h at e
+                            e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 4) << 16) | ((NB_ - 4) << 24), jo), 1);
                             h = fld(NB_ - 1 - e, 1);
+                        } else if constexpr (MD == 1) {  // p at 4 + 4 ca + cb, e at 2 + 4 ca + p, h at e
+                            const int p = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 6) << 8) | ((NB_ - 9) << 16) | ((NB_ - 10) << 24), jo), 1);
+                            e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 7) << 16) | ((NB_ - 7) << 24), jo) - p, 1);
+                            h = fld(NB_ - 1 - e, 1);
+                            pa = pb = p;
+                        } else if constexpr (!EQ) {
+                            if constexpr (PT == 1) {  // v3 at 8 + 10 ca + 3 cb (3 bits); e at 4 + 10 ca + idx; h at 2 e + c
+                                const int v3 = fld(tab8(((NB_ - 11) << 0) | ((NB_ - 14) << 8) | ((NB_ - 21) << 16) | ((NB_ - 24) << 24), jo), 3);
+                                const int idx = (0xEDEC >> (2 * v3)) & 3;
+                                cstar = idx >> 1;
+                                const int bsel = idx & 1;
+                                e = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 5) << 8) | ((NB_ - 15) << 16) | ((NB_ - 15) << 24), jo) - idx, 1);
+                                h = fld(NB_ - 1 - 2 * e - cstar, 1);
+                                pb = bsel ^ cstar;
+                                pa = bsel;
+                            } else {  // bsel at 4 + 6 ca + 2 cb + c; e at 2 + 6 ca + bsel; h at e
+                                const int bsel = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 7) << 8) | ((NB_ - 11) << 16) | ((NB_ - 13) << 24), jo) - cstar, 1);
+                                e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 9) << 16) | ((NB_ - 9) << 24), jo) - bsel, 1);
+                                h = fld(NB_ - 1 - e, 1);
+                                pb = bsel ^ cstar;
+                                pa = bsel;
+                            }
+                        } else {
+                            if constexpr (PT == 1) {  // c at 6 + 4 ca + cb; e at 4 + 4 ca + c; h at 2 e + c
+                                cstar = fld(tab8(((NB_ - 7) << 0) | ((NB_ - 8) << 8) | ((NB_ - 11) << 16) | ((NB_ - 12) << 24), jo), 1);
+                                e = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 5) << 8) | ((NB_ - 9) << 16) | ((NB_ - 9) << 24), jo) - cstar, 1);
+                                h = fld(NB_ - 1 - 2 * e - cstar, 1);
+                            } else {  // e at 2 + 2 ca + c; h at e
+                                e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 5) << 16) | ((NB_ - 5) << 24), jo) - cstar, 1);
+                                h = fld(NB_ - 1 - e, 1);
+                            }
+                            pa = pb = cstar;
                         }
-                        pa = pb = cstar;
-                    }
-                    s_rec[ph] = (uint32_t)(st | (gs << 10) | (e << 14) | (pa << 15) | (pb << 16));
-                    if (ph == mid_ph) {  // first tail-biting pass: only the state before mid_t is needed
-                        mid_val = (a.mid_t - 1) & 1 ? st : GE::mid(0, 2 * (jo >> 1) + e, qq, ll);
-                        stop = true;
-                        return;
-                    }
-                    const int Ln = X_.uni(2 * h + e);
-                    st = X_.uni(GE::start(Ln, qq, ll));  // state at step ta - 1
-                    sel = Ln;
-                    cstar = X_.uni(cstar);
-                    if (bnd) {  // sub-block start: the path came from the slot the merge chose
-                        gs = (int)X_.readlane(gv, Ln);
-                        sel = Ln + 4 * gs;
-                        nbnd -= sub;
-                        jb--;
-                    }
-                });
+                        s_rec[ph] = (uint32_t)(st | (gs << 10) | (e << 14) | (pa << 15) | (pb << 16));
+                        if (ph == mid_ph) {  // first tail-biting pass: only the state before mid_t is needed
+                            mid_val = (a.mid_t - 1) & 1 ? st : GE::mid(0, 2 * (jo >> 1) + e, qq, ll);
+                            stop = true;
+                            return;
+                        }
+                        const int Ln = X_.uni(2 * h + e);
+                        st = X_.uni(GE::start(Ln, qq, ll));  // state at step ta - 1
+                        sel = Ln;
+                        cstar = X_.uni(cstar);
+                        if (bnd) {  // sub-block start: the path came from the slot the merge chose
+                            gs = (int)X_.readlane(gv, Ln);
+                            sel = Ln + 4 * gs;
+                            nbnd -= sub;
+                            jb--;
+                        }
+                    });
+                }
+                X_.lds_sync();  // the records of chunk cc are written; chunk cc - 2 is in LDS; slot of cc + 1 free
             }
-            if (stop && lane == 0) a.mid_st[n] = mid_val;
-            X_.wait_loads(0);  // no copy may still land in this workgroup's LDS after it ends
-            if (lane == 0) {
+            if (wv == 1) X_.wait_loads(0);  // no copy may still land in this workgroup's LDS after it ends
+            if (wv == 0 && lane == 0) {
+                if (a.mid_st) a.mid_st[n] = mid_val;
                 a.best[n] = bi_all;
                 if (a.end_st) a.end_st[n] = bi_all % S;
             }
-            if (stop && a.mid_st) return;
+            if (a.mid_st) return;
         }
     }
-    if (!walked) {
+    if (!fast) {
         uint32_t* ring = (uint32_t*)(sm + SM.ring);
         const int nslot = SM.nslot, slot_words = SM.slot_words;
         const uint32_t* dummy = dm.bp;
@@ -1038,7 +1056,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
 
     // ---- reconstruction and code (tcq_viterbi.cu:662-682) -------------------------------------------
     float* rn = a.rec + (size_t)n * a.ld;
-    for (int t = lane; t < T; t += 64) {
+    for (int t = out_t0; t < T; t += out_dt) {
         const uint32_t rr = s_rec[t >> 1];
         const int so = rr & 1023, gg = (rr >> 10) & 15;
         // odd step: the phase's output state; even step: its intermediate state (block bits, e, ca, q, lane of so)
