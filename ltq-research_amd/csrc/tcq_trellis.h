@@ -578,6 +578,13 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
     int next_merge = sub, merge_j = 1;   // next sub-block boundary and its index
     // chunk c; FIRST: chunk 0, whose phase 0 starts the trellis (compile-time, so no other phase carries the
     // start-state selects)
+    // streamlined traceback (whole chunks, one block per lane, a second wavefront, a ring of at least 3 chunks):
+    // the last chunk's decision words then go straight from registers to the traceback's LDS ring
+    bool fast = false;
+    if constexpr (RB == 2) fast = T % CK == 0 && nthr >= 128 && SM.nslot >= 3;
+    uint32_t last_acc[NW];
+#pragma unroll
+    for (int w = 0; w < NW; w++) last_acc[w] = 0;
     auto chunk = [&](int c, auto FIRSTc) {
         constexpr bool FIRST = decltype(FIRSTc)::value;
 #pragma unroll
@@ -678,14 +685,20 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
         const int nwc = real == NPC ? NW : (rbits + 31) / 32;
         // word-major: word w of every lane of (slot g, wave q) is 64 consecutive u32 (coalesced stores)
         const long L0 = (long)c * chunk_words + (long)(g * Q + q) * nwc * 64 + lane;
+        if (fast && c == nchunk - 1) {
 #pragma unroll
-        for (int w = 0; w < NW; w++)
-            if (w < nwc) *dm.at(L0 + 64L * w) = acc[w];
+            for (int w = 0; w < NW; w++) last_acc[w] = acc[w];
+        } else {
+#pragma unroll
+            for (int w = 0; w < NW; w++)
+                if (w < nwc) *dm.at(L0 + 64L * w) = acc[w];
+        }
     };
     chunk(0, std::true_type{});
     for (int c = 1; c < nchunk; c++) chunk(c, std::false_type{});
 
     // ---- argmin over (g, s), lowest index on ties (tcq_viterbi.cu:561-578) ---------------------------
+    int bi_sel = 0;
     {
         const int s_end = a.tail ? s0 : -1;
         float bv = kSent;
@@ -716,21 +729,25 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
             s_ri[wv] = bi;
         }
         X_.sync();  // full barrier: also completes every wave's decision-word stores before the traceback
-        if (tid == 0) {
+        // every wavefront reduces the per-wavefront results across its lanes (no second barrier)
+        {
             const int nw = nthr / 64;
-            float cv = s_rv[0];
-            int ci = s_ri[0];
-            for (int i = 1; i < nw; i++)
-                if (s_rv[i] < cv || (s_rv[i] == cv && s_ri[i] < ci)) {
-                    cv = s_rv[i];
-                    ci = s_ri[i];
+            bv = lane < nw ? s_rv[lane] : kSent;
+            bi = lane < nw ? s_ri[lane] : 0x7fffffff;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float ov = X_.shfl_xor(bv, off);
+                const int oi = X_.shfl_xor(bi, off);
+                if (ov < bv || (ov == bv && oi < bi)) {
+                    bv = ov;
+                    bi = oi;
                 }
-            if (ci == 0x7fffffff) ci = 0;  // no candidate at or below the sentinel: the reference reads out of range
-            s_ctl[0] = ci;
+            }
         }
-        X_.lds_sync();
+        bi_sel = (int)X_.readlane((uint32_t)bi, 0);
+        if (bi_sel == 0x7fffffff) bi_sel = 0;  // no candidate at or below the sentinel: the reference reads out of range
     }
-    const int bi_all = (int)X_.readlane((uint32_t)s_ctl[0], 0);  // uniform: scalar registers
+    const int bi_all = X_.uni(bi_sel);  // uniform: scalar registers
 
     // ---- traceback (tcq_viterbi.cu:601-661) ----------------------------------------------------------
     // One LDS lookup per phase: the phase's output state names the (wave, lane) that computed it and the
@@ -742,8 +759,6 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
     // every matrix-path tile): wavefront 0 walks, wavefront 1 copies the decision words of the chunks ahead
     // global -> LDS, one barrier per chunk hands them over, and every thread writes the outputs. Otherwise
     // wavefront 0 alone walks (copying its own words) and writes the outputs, and the others are done.
-    bool fast = false;
-    if constexpr (RB == 2) fast = T % CK == 0 && nthr >= 128 && SM.nslot >= 3;
     if (!fast && wv != 0) return;
     int out_t0 = lane, out_dt = 64;
     if constexpr (RB == 2) {
@@ -783,10 +798,16 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
             auto count = [](int lo, int hi) { return hi >= lo ? hi - lo + 1 : 0; };
             const int mid_ph = a.mid_st ? (a.mid_t - 1) >> 1 : -1;
             const int kmax = a.mid_st ? nchunk - mid_ph / NPC : nchunk;  // chunks walked
-            // copier: chunks nchunk-1 .. nchunk-nslot+1 now; before the first barrier the two the walk reads
-            // first (its chunk and, from its last phase on, the one below) have landed
+            // copier: chunks nchunk-2 .. nchunk-nslot+1 now (the last one is written from registers); before the
+            // first barrier the two the walk reads first (its chunk and, from its last phase on, the one below)
+            // are in LDS
+            {  // the last chunk's words from registers (the forward pass's LDS is free since the argmin barrier)
+                uint32_t* slot = ring + ((nchunk - 1) % nslot) * slot_words;
+#pragma unroll
+                for (int w = 0; w < NW; w++) slot[((g * Q + q) * NW + w) * 64 + lane] = last_acc[w];
+            }
             if (wv == 1) {
-                for (int j = 0; j < nslot - 1 && nchunk - 1 - j >= 0; j++) issue(nchunk - 1 - j);
+                for (int j = 1; j < nslot - 1 && nchunk - 1 - j >= 0; j++) issue(nchunk - 1 - j);
                 X_.wait_loads(count(max_i(0, nchunk - nslot + 1), nchunk - 3) * nloads);
             }
             X_.lds_sync();
