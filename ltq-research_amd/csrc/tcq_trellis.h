@@ -556,9 +556,21 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
     float O[2][NB][4];
     uint32_t acc[NW];
 
-    // metrics of in-chunk phase PI (steps 2 PI, 2 PI + 1 of the chunk) for every (block, slot)
+    // metrics of in-chunk phase PI (steps 2 PI, 2 PI + 1 of the chunk) for every (block, slot), read through
+    // per-lane pointers into a chunk's table (set once per chunk; the phase and class are immediate offsets)
     float ma[NB][4][2], mb[NB][4][2];
-    auto load_metrics = [&](const float* tb, auto PIc) {
+    const float* pma[NB][4];
+    const float* pmb[NB][4];
+    auto point_metrics = [&](const float* tb) {
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                pma[b][j] = tb + offa[b][j];
+                pmb[b][j] = tb + offb[b][j];
+            }
+    };
+    auto load_metrics = [&](auto PIc) {
         constexpr int pi = decltype(PIc)::value;
 #pragma unroll
         for (int b = 0; b < NB; b++)
@@ -566,15 +578,23 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
             for (int j = 0; j < 4; j++)
 #pragma unroll
                 for (int p = 0; p < NP; p++) {
-                    ma[b][j][p] = tb[offa[b][j] + (2 * pi) * NL * NP + p];
-                    mb[b][j][p] = tb[offb[b][j] + (2 * pi + 1) * NL * NP + p];
+                    ma[b][j][p] = pma[b][j][(2 * pi) * NL * NP + p];
+                    mb[b][j][p] = pmb[b][j][(2 * pi + 1) * NL * NP + p];
                 }
     };
 
     tables(0);
     X_.lds_sync();
-    load_metrics(s_tabs, std::integral_constant<int, 0>{});
-    int xph = 0;                         // global phase counter (exchange buffer parity)
+    point_metrics(s_tabs);
+    load_metrics(std::integral_constant<int, 0>{});
+    // exchange addresses of this lane in buffer 0 / 1 (phases alternate, and every chunk has an even number of
+    // phases, so in-chunk phase pi uses buffer pi & 1): store at block 0 of the phase-end layout, loads at
+    // slot 0 of the phase-start layout (own gain slot, and gain slot 0 for the merge); blocks, slots, class
+    // planes and gain slots are immediate offsets
+    float* const xs_st0 = s_exch + (g * XF) * S + GE::end(0, 0, q, lane);
+    const float* const xs_ld0 = s_exch + (g * XF) * S + GE::start(0, q, lane);
+    const float* const xs_mg0 = s_exch + GE::start(0, q, lane);
+    const int xs_1 = SM.dbl ? SM.exch_floats : 0;
     int next_merge = sub, merge_j = 1;   // next sub-block boundary and its index
     // chunk c; FIRST: chunk 0, whose phase 0 starts the trellis (compile-time, so no other phase carries the
     // start-state selects)
@@ -589,7 +609,6 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
         constexpr bool FIRST = decltype(FIRSTc)::value;
 #pragma unroll
         for (int w = 0; w < NW; w++) acc[w] = 0;
-        const float* tb = s_tabs + (c & 1) * TF;
         const float* tbn = s_tabs + ((c + 1) & 1) * TF;
         int real = 0;  // phases of this chunk inside the tile
         static_for<0, NPC>([&](auto PIc) {
@@ -620,11 +639,18 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
             if (tn >= T) return;  // last phase: outputs stay in registers for the argmin
             // next phase's metrics: the tables were written before an earlier barrier, so the loads can fly
             // while this wave waits at the exchange barrier
-            if constexpr (pi + 1 < NPC) load_metrics(tb, std::integral_constant<int, pi + 1>{});
-            else load_metrics(tbn, std::integral_constant<int, 0>{});
+            if constexpr (pi + 1 < NPC) {
+                load_metrics(std::integral_constant<int, pi + 1>{});
+            } else {
+                point_metrics(tbn);
+                load_metrics(std::integral_constant<int, 0>{});
+            }
             // ---- exchange into the next phase's start layout (+ gain merge at a sub-block boundary) ----
             constexpr bool carry2 = TWO && PT == 0;  // phase A -> B carries two class planes
-            float* xb = s_exch + (SM.dbl ? (xph & 1) : 0) * SM.exch_floats;
+            const int xo = (pi & 1) ? xs_1 : 0;
+            float* const xst = xs_st0 + xo;
+            const float* const xld = xs_ld0 + xo;
+            const float* const xmg = xs_mg0 + xo;
             if (!SM.dbl) X_.lds_sync();  // single buffer: every wave has read the previous exchange
 #pragma unroll
             for (int b = 0; b < NB; b++)
@@ -635,10 +661,9 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
                     v4.y = O[cp][b][1];
                     v4.z = O[cp][b][2];
                     v4.w = O[cp][b][3];
-                    *(F4*)(xb + (g * XF + cp) * S + GE::end(b, 0, q, lane)) = v4;
+                    *(F4*)(xst + cp * S + (b << (8 + QB))) = v4;
                 }
             X_.lds_sync();
-            xph++;
             if (pi == 0 && c + 1 < nchunk) tables(c + 1);  // next chunk's table (its buffer was last read in chunk c-1)
             const bool at_sub = tn == next_merge;
             const int jm = merge_j;
@@ -654,10 +679,11 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         const int s = GE::start((j << (RB - 2)) | b, q, lane);
+                        const int so = ((j << (RB - 2)) | b) << (6 + QB);  // s - start(0, q, lane)
                         constexpr int GM = 16 / Q < 8 ? 16 / Q : 8;  // most gain slots this geometry serves
                         float v[GM];
 #pragma unroll
-                        for (int gg = 0; gg < GM; gg++) v[gg] = xb[(gg < G ? gg : 0) * XF * S + s];
+                        for (int gg = 0; gg < GM; gg++) v[gg] = gg < G ? xmg[gg * XF * S + so] : xmg[so];
                         float bv = v[0];
                         int bg = 0;
 #pragma unroll
@@ -676,7 +702,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
                     for (int b = 0; b < NB; b++)
 #pragma unroll
                         for (int j = 0; j < 4; j++)  // slot j of block b is register (j << (RB - 2)) | b
-                            I[cp][b][j] = xb[(g * XF + cp) * S + GE::start((j << (RB - 2)) | b, q, lane)];
+                            I[cp][b][j] = xld[cp * S + (((j << (RB - 2)) | b) << (6 + QB))];
             }
         });
         // ---- store this chunk's decision words (left-aligned), only the words holding real bits -------
