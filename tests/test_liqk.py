@@ -113,29 +113,34 @@ def test_gpu_ldlq_sub_matches_float64():
 
 
 @pytest.mark.gpu
-def test_gpu_quantize_rows_vs_oracle():
-    """TCQ275X2 rows [64, 512] with a real Hessian: the GPU quantizer against the CPU oracle on the same row
-    scale. The first sub-block's inputs are identical, so its codes are bit-exact; afterwards the error feedback
-    sums round differently (FMA vs the oracle's torch matmul), so codes may differ at near-ties only."""
+@pytest.mark.parametrize("spec,identity_h", [("TCQ275X2", False), ("TCQ275X", False), ("TCQ25X", False),
+                                             ("TCQ375X", False), ("TCQ3X3", True)])
+def test_gpu_quantize_rows_vs_oracle(spec, identity_h):
+    """Rows [64, 512] (C3 formats with a real Hessian; C2's TCQ3X3 with gain candidates and H = I): the GPU
+    quantizer against the CPU oracle on the same row scale. The first sub-block's inputs are identical, so its
+    codes are bit-exact; afterwards the error feedback sums round differently (FMA vs the oracle's torch
+    matmul), so codes may differ at near-ties only."""
     from oracle import liqk_ref
     from ltq_amd import liqk, rotation
     from ltq_amd.formats import TCQ_CONFIG, make_format
-    cfg = TCQ_CONFIG["TCQ275X2"]
+    cfg = TCQ_CONFIG[spec]
     M, K = 64, 512
     W, H = _synthetic(M, K)
+    if identity_h:
+        H = torch.eye(K)
     Wd, Hd = W.to(DEV), H.to(DEV)
     W_rot, H_rot, _ = rotation.compute_optimal_suh(Wd, Hd, seed=1337)
     U, diag_w, Ub_inv = liqk.factor_hessian(H_rot, 0.2)
-    print("quantize rows 64 x 512 TCQ275X2", flush=True)
+    print(f"quantize rows 64 x 512 {spec}", flush=True)
     liqk.PACK = {"groups": []}
     try:
-        d_full, W_hat = liqk._quantize_rows_tcq_ldlq(W_rot, U, Ub_inv, diag_w, "TCQ275X2")
+        d_full, W_hat = liqk._quantize_rows_tcq_ldlq(W_rot, U, Ub_inv, diag_w, spec)
         grp = liqk.PACK["groups"].pop()
     finally:
         liqk.PACK = None
     torch.cuda.synchronize()
     _, _, d_dev = liqk.row_scale(W_rot, cfg)
-    f = make_format("TCQ275X2")
+    f = make_format(spec)
     dr, Wh_ref, codes, _ = liqk_ref.quantize_rows_ref(W_rot.cpu(), U.cpu(), Ub_inv.cpu(), diag_w.cpu(), cfg,
                                                       f.gain_tab, d_rb_all=d_dev.cpu())
     idx, gi = grp["idx"].cpu(), grp["gi"].cpu()
