@@ -61,6 +61,14 @@ long ltq_slice_bytes(int R, int K, int fmt_K, int frac, int h, int sub);
 int ltq_pack_slice(const int16_t* idx, long ld_idx, const uint8_t* gi, long ld_gi, int R, int K, int fmt_K, int frac,
                    int h, int sub, uint8_t* out, long out_bytes, void* stream);
 
+/* Decodes a packed row slice [R, K] (the bytes ltq_pack_slice writes) into unscaled values out[R, K] (row
+ * stride ld_out): per position the tail-biting state from the code bits, its label from the masks m0 .. m3
+ * (n_masks of them), the level from the lsb stream and bit planes, the gain index of its sub-block, and
+ * value = gains[g] * lut[label * U + u]. Replaces the torch decoder src/ltq_file.py:119-147 (`decode_slice`). */
+int ltq_unpack_slice(const uint8_t* data, long data_bytes, int R, int K, int fmt_K, int frac, int h, int sub, int m0,
+                     int m1, int m2, int m3, int n_masks, const float* lut, const float* gains, float* out, long ld_out,
+                     void* stream);
+
 /* Bytes of one packed row ring of L positions (src/ltq_format.py:48-50, `tile_bytes(L)`, the ring's fp16 scale
  * excluded). L % 16 == 0, L <= 512, L % sub == 0; -1 otherwise. Host-only arithmetic. */
 long ltq_ring_bytes(int L, int fmt_K, int frac, int h, int sub);

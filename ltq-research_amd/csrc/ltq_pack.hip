@@ -237,3 +237,92 @@ extern "C" int ltq_pack_rings(const int16_t* idx, long ld_idx, const uint8_t* gi
                        ld_gi, n_rings, g, out);
     return (int)hipGetLastError();
 }
+
+// ---- decoding (src/ltq_file.py:119-147, the spec decoder) ------------------------------------------------
+// One wavefront per tile; lane l decodes positions 4 l .. 4 l + 3. The code bits give the tail-biting state of
+// every position (s_t = sum_j c_((t - j) mod 256) 2^j, j < 10), the state its label (bit 0 | parities of
+// (s >> 1) & mask_i), the lsb stream and the planes the level u, the gain stream the gain index of the sub-block:
+// value = gain[g] * lut[label * U + u] (the product the quantizer rounds its reconstruction with).
+namespace {
+
+__global__ __launch_bounds__(64 * kWaves) void unpack_kernel(const uint8_t* __restrict__ data, int R, int Kc, PackGeo g,
+                                                             int m0, int m1, int m2, int m3, int nm,
+                                                             const float* __restrict__ lut,
+                                                             const float* __restrict__ gains, float* __restrict__ out,
+                                                             long ld_out)
+{
+    constexpr int kMaxWords = 16 + 16 * 6 + 16 + 16;  // codes, planes (K <= 8), lsb, gains (h <= 8, sub >= 16)
+    __shared__ uint16_t s_w[kWaves][kMaxWords];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int kbs = Kc / 16;
+    const long T = (long)(R / 16) * kbs;
+    const int W = g.n[0] + g.n[1] + g.n[2] + g.n[3];
+    const int U = g.U;
+    for (long tile = (long)blockIdx.x * kWaves + wv; tile < T; tile += (long)gridDim.x * kWaves) {
+        for (int w = lane; w < W; w += 64) {
+            int reg, wr;
+            word_region(g, w, reg, wr);
+            s_w[wv][w] = *(const uint16_t*)(data + g.off[reg] + 2 * (tile * g.n[reg] + wr));
+        }
+        wave_sync();
+        const uint16_t* cw = s_w[wv];
+        const uint16_t* pw = cw + g.n[0];
+        const uint16_t* lw = pw + g.n[1];
+        const uint16_t* gw = lw + g.n[2];
+        auto bit = [](const uint16_t* ws, int i) -> uint32_t { return ((uint32_t)ws[i >> 4] >> (i & 15)) & 1u; };
+        const long rg = tile / kbs, kb = tile - rg * kbs;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 4 * lane + i;
+            uint32_t s = 0;
+#pragma unroll
+            for (int j = 0; j < 10; j++) s |= bit(cw, (t - j) & 255) << j;
+            const uint32_t sh = s >> 1;
+            uint32_t lb = (s & 1u) | ((uint32_t)(__builtin_popcount(sh & (uint32_t)m0) & 1) << 1);
+            if (nm > 1) lb |= (uint32_t)(__builtin_popcount(sh & (uint32_t)m1) & 1) << 2;
+            if (nm > 2) lb |= (uint32_t)(__builtin_popcount(sh & (uint32_t)m2) & 1) << 3;
+            if (nm > 3) lb |= (uint32_t)(__builtin_popcount(sh & (uint32_t)m3) & 1) << 4;
+            uint32_t u = 0;
+            if (g.K > 1) {
+                if (g.frac == 0) {
+                    u = bit(lw, t);
+                } else if (g.frac == 1) {
+                    u = bit(lw, t >> 1);
+                } else {  // three bits per quad, the fourth makes the quad's sum even
+                    const int q3 = 3 * (t >> 2), r = t & 3;
+                    u = r < 3 ? bit(lw, q3 + r) : (bit(lw, q3) ^ bit(lw, q3 + 1) ^ bit(lw, q3 + 2));
+                }
+                for (int p = 1; p < g.K - 1; p++) u |= bit(pw + (p - 1) * 16, t) << p;
+            }
+            float gain = 1.0f;
+            if (g.h) {
+                const int jb = (t / g.sub) * g.h;
+                uint32_t gi = 0;
+                for (int k = 0; k < g.h; k++) gi |= bit(gw, jb + k) << k;
+                gain = gains[gi];
+            }
+            out[(rg * 16 + (t >> 4)) * ld_out + kb * 16 + (t & 15)] = gain * lut[lb * U + u];
+        }
+        wave_sync();
+    }
+}
+
+}  // namespace
+
+extern "C" int ltq_unpack_slice(const uint8_t* data, long data_bytes, int R, int K, int fmt_K, int frac, int h, int sub,
+                                int m0, int m1, int m2, int m3, int n_masks, const float* lut, const float* gains,
+                                float* out, long ld_out, void* stream)
+{
+    const long need = ltq_slice_bytes(R, K, fmt_K, frac, h, sub);
+    if (need < 0 || data_bytes < need || ld_out < K || n_masks < 1 || n_masks > 4 || sub < 16 || fmt_K > 8)
+        return -1;
+    if (R == 0 || K == 0) return 0;
+    if (!data || !lut || (h && !gains) || !out) return -1;
+    const PackGeo g = pack_geo(R, K, fmt_K, frac, h, sub);
+    const long T = (long)(R / 16) * (K / 16);
+    long grid = (T + kWaves - 1) / kWaves;
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)grid), dim3(64 * kWaves), 0, (hipStream_t)stream, data, R, K, g, m0,
+                       m1, m2, m3, n_masks, lut, gains, out, ld_out);
+    return (int)hipGetLastError();
+}

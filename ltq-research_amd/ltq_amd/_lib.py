@@ -25,6 +25,7 @@ SIGNATURES = {
     # .ltq slice packing (src/ltq_file.py:79-96)
     "ltq_slice_bytes": (cl, [ci] * 6),
     "ltq_pack_slice": (ci, [vp, cl, vp, cl, ci, ci, ci, ci, ci, ci, vp, cl, vp]),
+    "ltq_unpack_slice": (ci, [vp, cl] + [ci] * 11 + [vp, vp, vp, cl, vp]),
     "ltq_ring_bytes": (cl, [ci, ci, ci, ci, ci]),
     "ltq_pack_rings": (ci, [vp, cl, vp, cl, cl, ci, ci, ci, ci, ci, vp, cl, vp]),
     # row scale and LDLQ sub-block feedback (src/liqk_v2.py:938-967)
