@@ -35,6 +35,18 @@ int tcq_viterbi(const float* x, const float* w, const float* tab, const float* g
 int lut_subs_quant(const float* xs, const float* dh, const float* lut, float* out, int S, float inv_step, float half_b,
                    int nb, void* stream);
 
+/* Both passes of the two-pass tail-biting Viterbi in one launch: the tcq_viterbi calls of
+ * src/tcq_proto.py:584-609 (tb_passes = 2, pass 1 with the same gain slots) fused, with identical results. The
+ * arguments are those of the closing pass (tail, T, rot, code, ...), with mid_buf [N] in the place of init_st:
+ * pass 1 (steps1 steps from rotation rot1, free start, no codes) leaves the state before its mid_t1 there and
+ * each workgroup starts its closing pass from it. Same return codes as tcq_viterbi. No counterpart in the
+ * reference, which launches the two passes separately. */
+int tcq_viterbi_tb(const float* x, const float* w, const float* tab, const float* gains, float* rec, uint32_t* bp,
+                   uint8_t* gsel, int* mid_buf, int* end_st, const float* tab_hi, const float* gains_hi,
+                   uint8_t* gcand, int* best, int* code, int tail, int N, int T, int S, int U, int G, int Gfull, int m,
+                   int sub, int U_hi, int mix, int m2, int m3, int m4, int nl, int ld, int rot, uint32_t* pbits, int pp,
+                   int steps1, int rot1, int mid_t1, void* stream);
+
 /* Normalized block FWHT-256 along rows: y[r, :] = FWHT256 of (x[r, :] op s), fp32 out.
  * Replaces the torch function src/iqk_format.py:153-170 (`fwht_inplace`) as called with a fused scale at
  * src/liqk_v2.py:438-439 (smode 1: x / s[col], smode 2: x * s[col], 0: none).

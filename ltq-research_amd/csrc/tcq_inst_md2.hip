@@ -3,11 +3,19 @@
 #include "tcq_launch.h"
 namespace ltq {
 template int launch<10, 2, 2, 4>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 2, 2, 4>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 2, 2, 8>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 2, 2, 8>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 2, 2, 16>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 2, 2, 16>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 2, 2, 32>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 2, 2, 32>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 3, 2, 4>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 3, 2, 4>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 3, 2, 8>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 3, 2, 8>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 3, 2, 16>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 3, 2, 16>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 3, 2, 32>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 3, 2, 32>(const TcqArgs&, const TcqArgs&, hipStream_t);
 }  // namespace ltq

@@ -3,11 +3,19 @@
 #include "tcq_launch.h"
 namespace ltq {
 template int launch<10, 2, 3, 4>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 2, 3, 4>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 2, 3, 8>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 2, 3, 8>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 2, 3, 16>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 2, 3, 16>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 2, 3, 32>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 2, 3, 32>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 3, 3, 4>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 3, 3, 4>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 3, 3, 8>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 3, 3, 8>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 3, 3, 16>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 3, 3, 16>(const TcqArgs&, const TcqArgs&, hipStream_t);
 template int launch<10, 3, 3, 32>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 3, 3, 32>(const TcqArgs&, const TcqArgs&, hipStream_t);
 }  // namespace ltq

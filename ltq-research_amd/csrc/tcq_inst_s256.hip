@@ -2,4 +2,5 @@
 #include "tcq_launch.h"
 namespace ltq {
 template int launch<8, 2, 0, 4>(const TcqArgs&, hipStream_t);
+template int launch_tb<8, 2, 0, 4>(const TcqArgs&, const TcqArgs&, hipStream_t);
 }  // namespace ltq

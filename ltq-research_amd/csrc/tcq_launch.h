@@ -36,6 +36,14 @@ struct GpuX {
     __device__ __forceinline__ int shfl_xor(int v, int m) const { return __shfl_xor(v, m, 64); }
     // a value every lane holds equally, pinned to a scalar register
     __device__ __forceinline__ int uni(int v) const { return __builtin_amdgcn_readfirstlane(v); }
+    // acquire at device scope: drops this CU's L1 lines, so global data rewritten since it was last read (by
+    // stores, which bypass L1) is fetched again
+    __device__ __forceinline__ void acquire() const { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+    // a global int another thread of the workgroup stored before the last sync(), read past the L1 cache
+    __device__ __forceinline__ int load_coherent(const int* p) const
+    {
+        return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     // lane l's value (l uniform), into a scalar register
     __device__ __forceinline__ uint32_t readlane(uint32_t v, int l) const
     {
@@ -75,6 +83,14 @@ __global__ __launch_bounds__(1024) void tcq_viterbi_kernel(TcqArgs a, int lds_ma
 
 int device_lds_max();
 
+// Both tail-biting passes of every tile in one launch.
+template <int NU, int RB, int MD, int NL>
+__global__ __launch_bounds__(1024) void tcq_viterbi_tb_kernel(TcqArgs a1, TcqArgs a2, int lds_max)
+{
+    GpuX x;
+    tcq_tile_tb<NU, RB, MD, NL>(a1, a2, x, lds_max);
+}
+
 template <int NU, int RB, int MD, int NL>
 int launch(const TcqArgs& a, hipStream_t stream)
 {
@@ -90,6 +106,27 @@ int launch(const TcqArgs& a, hipStream_t stream)
     }
     const int threads = 64 * a.G * Geo<NU, RB>::Q;
     hipLaunchKernelGGL((tcq_viterbi_kernel<NU, RB, MD, NL>), dim3(a.N), dim3(threads), L.total, stream, a, lds_max);
+    return 0;
+}
+
+template <int NU, int RB, int MD, int NL>
+int launch_tb(const TcqArgs& a1, const TcqArgs& a2, hipStream_t stream)
+{
+    const int lds_max = device_lds_max();
+    if (lds_max <= 0) return -1;
+    const Smem L1 = smem_layout<NU, RB, MD, NL>(a1.T, a1.G, a1.Gfull, a1.sub, lds_max);
+    const Smem L2 = smem_layout<NU, RB, MD, NL>(a2.T, a2.G, a2.Gfull, a2.sub, lds_max);
+    const int total = L1.total > L2.total ? L1.total : L2.total;
+    if (total > lds_max) return -1;
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void*)tcq_viterbi_tb_kernel<NU, RB, MD, NL>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
+        attr = true;
+    }
+    const int threads = 64 * a2.G * Geo<NU, RB>::Q;
+    hipLaunchKernelGGL((tcq_viterbi_tb_kernel<NU, RB, MD, NL>), dim3(a2.N), dim3(threads), total, stream, a1, a2,
+                       lds_max);
     return 0;
 }
 

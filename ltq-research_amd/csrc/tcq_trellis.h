@@ -66,6 +66,7 @@ struct TcqArgs {
     int mid_t, tail, N, T, S, U, G, Gfull, m, sub, U_hi, mix, m2, m3, m4, nl, ld, rot;
     uint32_t* pbits;       // scratch (reference size [N, T/2, G, S/32] for pp=1, [N, T/4, G, 9, S/32] for pp>=2)
     int pp;
+    int scratch_T = 0;     // > 0: the step count bp / pbits / gcand are sized for per tile (fused pass 1), else T
 };
 
 LTQ_DEV int parity32(uint32_t v) { return __builtin_popcount(v) & 1; }
@@ -406,12 +407,15 @@ struct DecMap {
 // The per-tile kernel body.
 // X provides: tid(), wave() (tid / 64, uniform), tile(), nthreads(), smem(), sync() (full barrier incl. global
 // memory), lds_sync() (barrier for LDS only), push_sign(acc, d), fmin(x, y), shfl_xor(v, mask) (within a
-// wavefront), readlane(v, l) (lane l's value, l uniform), load16(global src, LDS wave base) (asynchronous 16-byte
+// wavefront), readlane(v, l) (lane l's value, l uniform), uni(v) (a uniform value in a scalar register),
+// load_coherent(p) (a global int written by this workgroup before a sync()), acquire() (device-scope acquire:
+// invalidates this CU's L1), load16(global src, LDS wave base) (asynchronous 16-byte
 // global -> LDS copy landing at base + 16 * lane), wait_loads(n) (at most n such copies of this wave still
 // outstanding, n <= 63).
 // ------------------------------------------------------------------------------------------------
+// init_val >= 0: the start (and tail) state of the tile in place of init_st (the fused closing pass)
 template <int NU, int RB, int MD, int NL, class X>
-LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
+LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
 {
     using GE = Geo<NU, RB>;
     using MM = Md<MD, RB>;
@@ -425,6 +429,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
     const int T = a.T, G = a.G, sub = a.sub, U = a.U, U_hi = a.U_hi, mix = MD ? 0 : a.mix;
     const int Gf = a.Gfull, nsub = T / sub;
     const bool cand = a.gcand != nullptr;
+    const int Ts = a.scratch_T > 0 ? a.scratch_T : T;  // per-tile scratch layout (a fused pass 1 shares pass 2's)
     const Masks mk{a.m, a.m2, a.m3, a.m4, NL};
     const Smem SM = smem_layout<NU, RB, MD, NL>(T, G, Gf, sub, lds_max);
     char* sm = (char*)X_.smem();
@@ -459,7 +464,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
         s_gain[tid] = a.gains[tid];
         s_gain_hi[tid] = a.gains_hi[tid];
     }
-    const int s0 = a.init_st ? a.init_st[n] : -1;
+    const int s0 = init_val >= 0 ? init_val : (a.init_st ? a.init_st[n] : -1);
     X_.lds_sync();
 
     // ---- gain candidates: the G gains of lowest scalar error per sub-block (tcq_viterbi.cu:155-180) ----
@@ -489,7 +494,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
                     }
                 used |= 1u << bg;
                 s_gc[tid * G + c] = (uint8_t)bg;
-                a.gcand[((size_t)n * nsub + tid) * G + c] = (uint8_t)bg;
+                a.gcand[((size_t)n * (Ts / sub) + tid) * G + c] = (uint8_t)bg;
             }
         }
         X_.lds_sync();
@@ -539,9 +544,9 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
             ok[b][j] = s0 < 0 || (sm1 >> 1) == (s0 & (HALF - 1));
         }
 
-    const DecMap dm{a.bp + (size_t)n * T * G * (S / 32),
-                    a.pbits ? a.pbits + (size_t)n * (scratch_words(T, G, S, a.pp) - (long)T * G * (S / 32)) : nullptr,
-                    (long)T * G * (S / 32)};
+    const DecMap dm{a.bp + (size_t)n * Ts * G * (S / 32),
+                    a.pbits ? a.pbits + (size_t)n * (scratch_words(Ts, G, S, a.pp) - (long)Ts * G * (S / 32)) : nullptr,
+                    (long)Ts * G * (S / 32)};
     const int nph = T / 2;
     const int nchunk = (nph + NPC - 1) / NPC;
     const long chunk_words = (long)G * Q * 64 * NW;
@@ -1140,6 +1145,28 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max)
 #undef LTQ_PUSH0
 
 
+// Both tail-biting passes of one tile in one workgroup (the two tcq_viterbi calls of src/tcq_proto.py:584-609
+// with tb_passes = 2, same gain slots): pass 1 leaves the state before its mid_t in a1.mid_st; after a full
+// barrier (the pass-1 walk done, the store visible) every thread reads it back coherently and pass 2 starts and
+// closes there. The two passes lay LDS out independently; the barrier ends every use of pass 1's layout.
+template <int NU, int RB, int MD, int NL, class X>
+LTQ_DEV void tcq_tile_tb(const TcqArgs& a1, const TcqArgs& a2, X& X_, int lds_max)
+{
+    int init = -1;
+    // one copy of the tile body, run twice (two inlined copies would double the code the instruction cache holds)
+#pragma nounroll
+    for (int p = 0; p < 2; p++) {
+        tcq_tile<NU, RB, MD, NL>(p == 0 ? a1 : a2, X_, lds_max, init);
+        if (p == 0) {
+            X_.sync();
+            // pass 1's traceback pulled its decision words through this CU's L1; pass 2 rewrites the same
+            // scratch (stores bypass L1), so the stale lines must go before pass 2's traceback reads them back
+            X_.acquire();
+            init = X_.uni(X_.load_coherent(a1.mid_st + X_.tile()));
+        }
+    }
+}
+
 // ---- host side: argument validation and dispatch, shared by the gfx950 entry point and the CPU emulation ----
 
 // The reference's validation (tcq_viterbi.cu:748-751, 762-763) plus this implementation's limits.
@@ -1164,7 +1191,8 @@ int tcq_dispatch(const TcqArgs& a, const F& f)
 {
     auto go = [&](auto nu, auto rb, auto md) -> int {
         constexpr int NU = decltype(nu)::value, RB = decltype(rb)::value, MD = decltype(md)::value;
-        if (needed_words<NU, RB, MD>(a.T, a.G) > scratch_words(a.T, a.G, a.S, a.pp)) return -1;
+        if (needed_words<NU, RB, MD>(a.T, a.G) > scratch_words(a.scratch_T > 0 ? a.scratch_T : a.T, a.G, a.S, a.pp))
+            return -1;
         switch (a.nl) {
             case 4: return f.template run<NU, RB, MD, 4>();
             case 8: return f.template run<NU, RB, MD, 8>();
@@ -1177,7 +1205,8 @@ int tcq_dispatch(const TcqArgs& a, const F& f)
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
     if (a.S == 256) {
-        if (needed_words<8, 2, 0>(a.T, a.G) > scratch_words(a.T, a.G, a.S, a.pp)) return -1;
+        if (needed_words<8, 2, 0>(a.T, a.G) > scratch_words(a.scratch_T > 0 ? a.scratch_T : a.T, a.G, a.S, a.pp))
+            return -1;
         return f.template run<8, 2, 0, 4>();
     }
     const bool r3 = a.G > 4;

@@ -15,7 +15,9 @@
 namespace ltq {
 
 // instantiated in tcq_inst_*.hip (compiled in parallel)
-#define LTQ_EXT(NU, RB, MD, NL) extern template int launch<NU, RB, MD, NL>(const TcqArgs&, hipStream_t);
+#define LTQ_EXT(NU, RB, MD, NL)                                                \
+    extern template int launch<NU, RB, MD, NL>(const TcqArgs&, hipStream_t); \
+    extern template int launch_tb<NU, RB, MD, NL>(const TcqArgs&, const TcqArgs&, hipStream_t);
 #define LTQ_EXT_MD(MD)                                                                                \
     LTQ_EXT(10, 2, MD, 4) LTQ_EXT(10, 2, MD, 8) LTQ_EXT(10, 2, MD, 16) LTQ_EXT(10, 2, MD, 32)        \
     LTQ_EXT(10, 3, MD, 4) LTQ_EXT(10, 3, MD, 8) LTQ_EXT(10, 3, MD, 16) LTQ_EXT(10, 3, MD, 32)
@@ -46,6 +48,26 @@ struct GpuLaunch {
     }
 };
 
+// capacity check only (tcq_dispatch rejects what does not fit the scratch before calling run)
+struct GpuLaunchTbCheck {
+    template <int NU, int RB, int MD, int NL>
+    int run() const
+    {
+        return 0;
+    }
+};
+
+struct GpuLaunchTb {
+    const TcqArgs& a1;
+    const TcqArgs& a2;
+    hipStream_t st;
+    template <int NU, int RB, int MD, int NL>
+    int run() const
+    {
+        return launch_tb<NU, RB, MD, NL>(a1, a2, st);
+    }
+};
+
 }  // namespace ltq
 
 using ltq::TcqArgs;
@@ -63,6 +85,33 @@ extern "C" int tcq_viterbi(const float* x, const float* w, const float* tab, con
     if (tcq_check(a) != 0 || (getenv("TCQ_BLOCK") && nl != 4)) return -1;
     if (N <= 0) return N == 0 ? (int)hipErrorInvalidConfiguration : -1;  // a 0-block launch, as the reference gets
     const int rc = tcq_dispatch(a, GpuLaunch{a, (hipStream_t)stream});
+    if (rc != 0) return rc;
+    return (int)hipGetLastError();
+}
+
+// Both tail-biting passes in one launch (the two calls of src/tcq_proto.py:584-609 with tb_passes = 2 and the
+// same gain slots): the arguments of the closing pass (init_st: the [N] buffer pass 1 leaves its middle states
+// in, read back by the same workgroup) and pass 1's steps, rotation and mid_t.
+extern "C" int tcq_viterbi_tb(const float* x, const float* w, const float* tab, const float* gains, float* rec,
+                              uint32_t* bp, uint8_t* gsel, int* mid_buf, int* end_st, const float* tab_hi,
+                              const float* gains_hi, uint8_t* gcand, int* best, int* code, int tail, int N, int T, int S,
+                              int U, int G, int Gfull, int m, int sub, int U_hi, int mix, int m2, int m3, int m4,
+                              int nl, int ld, int rot, uint32_t* pbits, int pp, int steps1, int rot1, int mid_t1,
+                              void* stream)
+{
+    using namespace ltq;
+    TcqArgs a2{x, w, tab, gains, rec, bp, gsel, mid_buf, end_st, tab_hi, gains_hi, gcand, best, code, nullptr,
+               0, tail, N, T, S, U, G, Gfull, m, sub, U_hi, mix, m2, m3, m4, nl, ld, rot, pbits, pp};
+    TcqArgs a1{x, w, tab, gains, rec, bp, gsel, nullptr, nullptr, tab_hi, gains_hi, gcand, best, nullptr, mid_buf,
+               mid_t1, 0, N, steps1, S, U, G, Gfull, m, sub, U_hi, mix, m2, m3, m4, nl, ld, rot1, pbits, pp};
+    a1.scratch_T = T;  // pass 1 works inside the scratch sized for the closing pass
+    if (!mid_buf || steps1 <= 0 || steps1 > T || mid_t1 <= 0 || mid_t1 > steps1) return -1;
+    if (tcq_check(a1) != 0 || tcq_check(a2) != 0 || (getenv("TCQ_BLOCK") && nl != 4)) return -1;
+    if (N <= 0) return N == 0 ? (int)hipErrorInvalidConfiguration : -1;
+    // pass 1 must fit the scratch of the instance pass 2 selects (it has fewer steps)
+    int rc = tcq_dispatch(a1, GpuLaunchTbCheck{});
+    if (rc != 0) return rc;
+    rc = tcq_dispatch(a2, GpuLaunchTb{a1, a2, (hipStream_t)stream});
     if (rc != 0) return rc;
     return (int)hipGetLastError();
 }

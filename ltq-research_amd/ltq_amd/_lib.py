@@ -17,6 +17,8 @@ vp, ci, cf, cl = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_long
 SIGNATURES = {
     # src/cuda/tcq_viterbi.cu:743-746; ctypes argtypes as src/tcq_proto.py:529
     "tcq_viterbi": (ci, [vp] * 15 + [ci] * 18 + [vp, ci, vp]),
+    # both tail-biting passes in one launch (no reference counterpart; the two calls of src/tcq_proto.py:584-609)
+    "tcq_viterbi_tb": (ci, [vp] * 14 + [ci] * 17 + [vp, ci, ci, ci, ci, vp]),
     # src/cuda/tcq_viterbi.cu:806-807; src/tcq_proto.py:531-532
     "lut_subs_quant": (ci, [vp] * 4 + [ci, cf, cf, ci, vp]),
     # FWHT-256 (src/iqk_format.py:153-170), rows with a fused scale / columns

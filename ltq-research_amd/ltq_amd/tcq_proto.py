@@ -61,11 +61,14 @@ def viterbi_ub_cuda(x: torch.Tensor, small: torch.Tensor, K: int, nu: int, m: in
                     gains_hi: torch.Tensor | None = None, mix: int = 0, n_cand: int = 0, return_code: bool = False,
                     tail_biting: bool = False, tb_passes: int = 2, tb_cand1: int = 0, tb_window: int = 0,
                     m_extra: tuple = (), pair_parity=False, _mid: int = 0, _tail: bool = False, _steps: int = 0,
-                    _rot: int = 0, _raw_code: bool = False):
+                    _rot: int = 0, _raw_code: bool = False, _fuse: bool = False, _fused: tuple | None = None):
     """Joint (gain, trellis) Viterbi over tiles x [N, T] on the GPU; see src/tcq_proto.py:567-583 for the meaning
     of every argument. Returns rec [N, T]; or (rec, gain index, level index) with return_code; or (rec, end
     state) with return_end_state; or (rec, mid state) for an internal first tail-biting pass. _raw_code with
-    return_code gives (rec, code) with the kernel's packed int32 code (gain index << 16 | level index)."""
+    return_code gives (rec, code) with the kernel's packed int32 code (gain index << 16 | level index).
+    _fuse=True runs both tail-biting passes (same gain slots) in one launch (tcq_viterbi_tb, identical results).
+    It is off by default: on gfx950 the fused kernel measures ~30 us slower per 4096-tile sub-block than the two
+    launches (the pass loop keeps both argument sets live, 140 SGPR spills)."""
     _lib.require_device(x)
     if tail_biting:
         N, T = x.shape
@@ -76,6 +79,10 @@ def viterbi_ub_cuda(x: torch.Tensor, small: torch.Tensor, K: int, nu: int, m: in
         # pass 1 only locates the path state in the middle of the tile: over the window [h-w, h+w) when
         # tb_window > 0 (shift + step count, no copies), over the whole tile otherwise
         nc1 = tb_cand1 if tb_cand1 else n_cand
+        if tb_passes == 2 and nc1 == n_cand and _fuse:  # both passes in one launch
+            fused = (2 * tb_window, h - tb_window, tb_window) if tb_window else (T, 0, h)
+            return viterbi_ub_cuda(xf, small, K, nu, m, gains, wts=w_full, n_cand=n_cand, return_code=return_code,
+                                   _tail=True, _rot=h % T, _raw_code=_raw_code, _fused=fused, **common)
         if tb_window:
             _, mid = viterbi_ub_cuda(xf, small, K, nu, m, gains, wts=w_full, n_cand=nc1, _mid=tb_window,
                                      _steps=2 * tb_window, _rot=h - tb_window, **common)
@@ -132,11 +139,21 @@ def viterbi_ub_cuda(x: torch.Tensor, small: torch.Tensor, K: int, nu: int, m: in
         if (_launch_count // 2) % LAUNCH_SAMPLE == 0:
             evs = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             evs[0].record(torch.cuda.current_stream())
-        _launch_count += 1
-    rc = _lib.lib().tcq_viterbi(p(xf), p(w), p(tab), p(g), p(rec), p(bp), p(gsel), p(init), p(end), p(tab_hi), p(g_hi),
-                                p(cand), p(best), p(code), p(mid), _mid, int(_tail), N, T, S, U, G_run, Gfull, m, sub,
-                                tab_hi.numel() // nl, mix if small_hi is not None else 0, me[0], me[1], me[2], nl, ld,
-                                _rot, p(pbits), pp, _lib.stream_ptr())
+        _launch_count += 2 if _fused else 1
+    mix_arg = mix if small_hi is not None else 0
+    if _fused:  # both tail-biting passes: pass 1's middle states land in mid_buf, the closing pass starts there
+        if init_state is not None:
+            raise ValueError("the fused tail-biting launch computes its own start states")
+        mid_buf = torch.empty(N, dtype=torch.int32, device=dev)
+        rc = _lib.lib().tcq_viterbi_tb(p(xf), p(w), p(tab), p(g), p(rec), p(bp), p(gsel), p(mid_buf), p(end),
+                                       p(tab_hi), p(g_hi), p(cand), p(best), p(code), int(_tail), N, T, S, U, G_run,
+                                       Gfull, m, sub, tab_hi.numel() // nl, mix_arg, me[0], me[1], me[2], nl, ld, _rot,
+                                       p(pbits), pp, _fused[0], _fused[1], _fused[2], _lib.stream_ptr())
+    else:
+        rc = _lib.lib().tcq_viterbi(p(xf), p(w), p(tab), p(g), p(rec), p(bp), p(gsel), p(init), p(end), p(tab_hi),
+                                    p(g_hi), p(cand), p(best), p(code), p(mid), _mid, int(_tail), N, T, S, U, G_run,
+                                    Gfull, m, sub, tab_hi.numel() // nl, mix_arg, me[0], me[1], me[2], nl, ld, _rot,
+                                    p(pbits), pp, _lib.stream_ptr())
     if rc != 0:
         raise RuntimeError(f"tcq_viterbi: HIP error code {rc}")
     if evs is not None:

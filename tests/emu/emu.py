@@ -32,6 +32,8 @@ def lib(asan: bool = False):
         L = ctypes.CDLL(str(so))
         L.tcq_viterbi_emu.restype = ctypes.c_int
         L.tcq_viterbi_emu.argtypes = [ctypes.c_void_p] * 15 + [ctypes.c_int] * 18 + [ctypes.c_void_p, ctypes.c_int]
+        L.tcq_viterbi_tb_emu.restype = ctypes.c_int
+        L.tcq_viterbi_tb_emu.argtypes = [ctypes.c_void_p] * 14 + [ctypes.c_int] * 17 + [ctypes.c_void_p] + [ctypes.c_int] * 4
         _LIB[asan] = L
     return _LIB[asan]
 
@@ -77,3 +79,42 @@ def tcq_viterbi(x, w, tab, gains, *, init_st=None, tab_hi=None, gains_hi=None, n
     if rc != 0:
         raise RuntimeError(f"tcq_viterbi_emu: error code {rc}")
     return {"rec": rec, "code": code, "best": best, "end": end, "mid": mid, "gcand": cand}
+
+
+def tcq_viterbi_tb(x, w, tab, gains, *, n_cand=0, S=1024, U=None, m=359, sub=16, m_extra=(), pp=0, window=0,
+                   asan=False):
+    """Both tail-biting passes in one emulated launch (the fused entry point): pass 1 over the window
+    [h - window, h + window) (the whole tile when window is 0) for the middle state, then the closed pass from it
+    at rotation h. Returns rec, code and the closing pass's best (g, s)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    N, T = x.shape
+    h = T // 2
+    nl = 4 << len(m_extra)
+    tab = np.ascontiguousarray(tab, np.float32)
+    gains = np.ascontiguousarray(gains, np.float32)
+    U = tab.size // nl if U is None else U
+    Gfull = gains.size
+    G = n_cand if 0 < n_cand < Gfull else Gfull
+    rec = np.zeros((N, T), np.float32)
+    bp = np.zeros((N, T, G, S // 32), np.int32)
+    gsel = np.zeros((N, max(T // sub, 1), S), np.uint8)
+    best = np.zeros(N, np.int32)
+    code = np.zeros((N, T), np.int32)
+    mid = np.zeros(N, np.int32)
+    cand = np.zeros((N, T // sub, G), np.uint8) if G < Gfull else None
+    if pp >= 2:
+        pbits = np.zeros((N, T // 4, G, 9, S // 32), np.int32)
+    elif pp == 1:
+        pbits = np.zeros((N, T // 2, G, S // 32), np.int32)
+    else:
+        pbits = None
+    me = (list(m_extra) + [0, 0, 0])[:3]
+    steps1, rot1, mid1 = (2 * window, h - window, window) if window else (T, 0, h)
+    rc = lib(asan).tcq_viterbi_tb_emu(
+        _p(x), _p(w), _p(tab), _p(gains), _p(rec), _p(bp), _p(gsel), _p(mid), None, _p(tab), _p(gains), _p(cand),
+        _p(best), _p(code), 1, N, T, S, U, G, Gfull, m, sub, U, 0, me[0], me[1], me[2], nl, T, h % T, _p(pbits),
+        int(pp), steps1, rot1, mid1)
+    if rc != 0:
+        raise RuntimeError(f"tcq_viterbi_tb_emu: error code {rc}")
+    return {"rec": rec, "code": code, "best": best}

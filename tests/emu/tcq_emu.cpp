@@ -60,6 +60,8 @@ struct CpuX {
     }
     int shfl_xor(int v, int m) const { return (int)xor_lane((uint32_t)v, m); }
     int uni(int v) const { return v; }
+    int load_coherent(const int* p) const { return *p; }
+    void acquire() const {}
     uint32_t readlane(uint32_t v, int l) const
     {
         const int w = tid_ >> 6;
@@ -112,6 +114,70 @@ struct CpuRun {
         return 0;
     }
 };
+
+struct CpuRunTb {
+    const TcqArgs& a1;
+    const TcqArgs& a2;
+    template <int NU, int RB, int MD, int NL>
+    int run() const
+    {
+        const Smem L1 = smem_layout<NU, RB, MD, NL>(a1.T, a1.G, a1.Gfull, a1.sub, kLdsMax);
+        const Smem L2 = smem_layout<NU, RB, MD, NL>(a2.T, a2.G, a2.Gfull, a2.sub, kLdsMax);
+        const int total = L1.total > L2.total ? L1.total : L2.total;
+        if (total > kLdsMax) return -1;
+        const int nthr = 64 * a2.G * Geo<NU, RB>::Q;
+        const int nw = nthr / 64;
+        std::vector<char> smem(total + 64);
+        for (int n = 0; n < a2.N; n++) {
+            std::memset(smem.data(), 0xA5, smem.size());
+            std::barrier<> blk(nthr);
+            std::vector<std::unique_ptr<std::barrier<>>> wv;
+            std::vector<std::barrier<>*> ptrs;
+            for (int g = 0; g < nw; g++) {
+                wv.emplace_back(new std::barrier<>(64));
+                ptrs.push_back(wv.back().get());
+            }
+            std::vector<uint32_t> xch(nthr);
+            std::vector<std::thread> th;
+            for (int t = 0; t < nthr; t++) {
+                th.emplace_back([&, t]() {
+                    CpuX x{t, n, nthr, smem.data(), &blk, ptrs.data(), xch.data()};
+                    tcq_tile_tb<NU, RB, MD, NL>(a1, a2, x, kLdsMax);
+                });
+            }
+            for (auto& t : th) t.join();
+        }
+        return 0;
+    }
+};
+
+struct CpuCheck {
+    template <int NU, int RB, int MD, int NL>
+    int run() const
+    {
+        return 0;
+    }
+};
+
+extern "C" int tcq_viterbi_tb_emu(const float* x, const float* w, const float* tab, const float* gains, float* rec,
+                                  uint32_t* bp, uint8_t* gsel, int* mid_buf, int* end_st, const float* tab_hi,
+                                  const float* gains_hi, uint8_t* gcand, int* best, int* code, int tail, int N, int T,
+                                  int S, int U, int G, int Gfull, int m, int sub, int U_hi, int mix, int m2, int m3,
+                                  int m4, int nl, int ld, int rot, uint32_t* pbits, int pp, int steps1, int rot1,
+                                  int mid_t1)
+{
+    TcqArgs a2{x, w, tab, gains, rec, bp, gsel, mid_buf, end_st, tab_hi, gains_hi, gcand, best, code, nullptr,
+               0, tail, N, T, S, U, G, Gfull, m, sub, U_hi, mix, m2, m3, m4, nl, ld, rot, pbits, pp};
+    TcqArgs a1{x, w, tab, gains, rec, bp, gsel, nullptr, nullptr, tab_hi, gains_hi, gcand, best, nullptr, mid_buf,
+               mid_t1, 0, N, steps1, S, U, G, Gfull, m, sub, U_hi, mix, m2, m3, m4, nl, ld, rot1, pbits, pp};
+    a1.scratch_T = T;  // pass 1 works inside the scratch sized for the closing pass
+    if (!mid_buf || steps1 <= 0 || steps1 > T || mid_t1 <= 0 || mid_t1 > steps1) return -1;
+    if (tcq_check(a1) != 0 || tcq_check(a2) != 0) return -1;
+    if (N <= 0) return N == 0 ? 0 : -1;
+    const int rc = tcq_dispatch(a1, CpuCheck{});
+    if (rc != 0) return rc;
+    return tcq_dispatch(a2, CpuRunTb{a1, a2});
+}
 
 extern "C" int tcq_viterbi_emu(const float* x, const float* w, const float* tab, const float* gains, float* rec,
                                uint32_t* bp, uint8_t* gsel, const int* init_st, int* end_st, const float* tab_hi,

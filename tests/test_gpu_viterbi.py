@@ -169,3 +169,24 @@ def test_rejected_configs_raise(tp):
         tp.viterbi_ub_cuda(x, torch.zeros(16, device=DEV), 3, 10, 359, torch.ones(5, device=DEV))  # G = 5
     with pytest.raises(RuntimeError):
         tp.viterbi_ub_cuda(x, torch.zeros(16, device=DEV), 3, 10, 359, None, sub=3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,window", [("TCQ275X2", 32), ("TCQ25X", 0), ("TCQ3X3", 32), ("TCQ4X", 16)])
+def test_gpu_fused_tail_biting_equals_two_launches(name, window):
+    """The fused two-pass launch (tcq_viterbi_tb) gives exactly the two separate launches' results."""
+    from ltq_amd.formats import TCQ_CONFIG, make_format
+    from ltq_amd.tcq_proto import viterbi_ub_cuda
+    f, cfg = make_format(name), TCQ_CONFIG[name]
+    g = torch.Generator().manual_seed(9)
+    x = (torch.randn((300, 256), generator=g) * 1.1).cuda()
+    w = (torch.rand((300, 256), generator=g) + 0.5).cuda()
+    kw = dict(sub=f.sub, wts=w, n_cand=cfg.get("n_cand", 0), tail_biting=True, tb_window=window,
+              m_extra=f.masks[1:], pair_parity=f.frac, return_code=True)
+    lut, gains = torch.tensor(f.lut).cuda(), torch.tensor(f.gain_tab).cuda()
+    print(f"fused vs two launches {name} w={window}", flush=True)
+    a = viterbi_ub_cuda(x, lut, f.K, 10, f.masks[0], gains, _fuse=True, **kw)
+    b = viterbi_ub_cuda(x, lut, f.K, 10, f.masks[0], gains, _fuse=False, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(a[0].view(torch.int32), b[0].view(torch.int32))
+    assert torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])

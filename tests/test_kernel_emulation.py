@@ -72,3 +72,37 @@ def test_emulated_kernel_matches_oracle(oracle, ci):
         assert np.array_equal(o["rec"].view(np.uint32), e["rec"].view(np.uint32))
     if o["gcand"] is not None:
         assert np.array_equal(o["gcand"], e["gcand"])
+
+
+TB_CASES = [
+    dict(pp=2, ext=(241,), G=4, T=256, window=32),          # the matrix path (TCQ275X2)
+    dict(pp=2, ext=(), G=4, T=64, window=0, U=8),           # whole-tile pass 1
+    dict(pp=1, ext=(241,), G=2, T=128, window=16),          # D2
+    dict(pp=3, ext=(), G=2, T=64, window=16),               # EQ
+    dict(pp=0, ext=(241, 40), G=4, Gfull=8, T=128, window=32, n_cand=4),  # candidates
+    dict(pp=0, ext=(), G=8, T=64, window=16),               # G = 8: the general walker
+]
+
+
+@pytest.mark.parametrize("ci", range(len(TB_CASES)))
+def test_emulated_fused_tail_biting_matches_two_pass_driver(ci):
+    """Both passes in one launch (tcq_tile_tb) against the oracle's two-pass driver (src/tcq_proto.py:584-609)."""
+    import emu
+    from oracle import ref
+    c = TB_CASES[ci]
+    rng = np.random.default_rng(100 + ci)
+    nl = 4 << len(c["ext"])
+    U = c.get("U", 4)
+    Gf = c.get("Gfull", c["G"])
+    N, T = 2, c["T"]
+    tab = rng.standard_normal(nl * U).astype(np.float32)
+    gains = (2.0 ** ((np.arange(Gf) - (Gf - 1) / 2) * 0.22)).astype(np.float32)
+    x = (rng.standard_normal((N, T)) * 1.2).astype(np.float32)
+    w = (rng.random((N, T)) + 0.5).astype(np.float32)
+    e = emu.tcq_viterbi_tb(x, w, tab, gains, n_cand=c.get("n_cand", 0), m_extra=c["ext"], pp=c["pp"],
+                           window=c["window"])
+    rec, gi, ix = ref.viterbi_ub_cuda_ref(x, tab, int(np.log2(U)) + 1, 10, 359, gains, sub=16, wts=w,
+                                          n_cand=c.get("n_cand", 0), tail_biting=True, tb_window=c["window"],
+                                          m_extra=c["ext"], pair_parity=c["pp"], return_code=True)
+    assert np.array_equal(e["rec"].view(np.uint32), np.asarray(rec, np.float32).view(np.uint32))
+    assert np.array_equal(e["code"], (np.asarray(gi, np.int64) << 16 | np.asarray(ix, np.int64)).astype(np.int32))
