@@ -117,6 +117,17 @@ int ltq_ldlq_sub(float* wk, long ldw, const float* rec, const float* d, long ldd
                  const float* ublk, long ldu, int ib, float* G, long ldg, float* xnext, long M, const int* code,
                  int16_t* idx, long ld_idx, uint8_t* gi, long ld_gi, void* stream);
 
+/* Input-covariance accumulation, the _CovAccumulator.add of src/liqk_v2.py:218-228 for bf16 (f16 = 0) or fp16
+ * (f16 = 1) activations: H += X^T X for X [n, K] (element type 16-bit, row stride ldx >= K), fp32 accumulation
+ * over the batch on the matrix cores, added into the fp64 running sum H [K, K] (row stride ldh). Only the
+ * 128 x 128 tiles on and below the diagonal of H are updated; ltq_cov_finalize reads the lower triangle.
+ * n == 0 is a no-op. The reference's fp32 path (torch GEMM) has no counterpart here. */
+int ltq_cov_accumulate(const void* X, long n, int K, long ldx, int f16, double* H, long ldh, void* stream);
+
+/* The get() of src/liqk_v2.py:230-231: out[i][j] (fp32, row stride ldo) = (float)(H[max(i,j)][min(i,j)] * inv_n)
+ * with inv_n = 1.0 / max(count, 1) in fp64 (torch's device division of an fp64 tensor by an integer). */
+int ltq_cov_finalize(const double* H, int K, long ldh, double inv_n, float* out, long ldo, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

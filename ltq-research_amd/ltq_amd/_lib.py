@@ -11,7 +11,7 @@ from pathlib import Path
 _SO = Path(__file__).resolve().parent / "libltq_hip.so"
 _LIB = None
 
-vp, ci, cf, cl = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_long
+vp, ci, cf, cl, cd = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_long, ctypes.c_double
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -31,6 +31,9 @@ SIGNATURES = {
     "ltq_ring_bytes": (cl, [ci, ci, ci, ci, ci]),
     "ltq_pack_rings": (ci, [vp, cl, vp, cl, cl, ci, ci, ci, ci, ci, vp, cl, vp]),
     # row scale and LDLQ sub-block feedback (src/liqk_v2.py:938-967)
+    # src/liqk_v2.py:207-231 (_CovAccumulator.add / get)
+    "ltq_cov_accumulate": (ci, [vp, cl, ci, cl, ci, vp, cl, vp]),
+    "ltq_cov_finalize": (ci, [vp, ci, cl, cd, vp, cl, vp]),
     "ltq_row_scale": (ci, [vp, cl, cl, cl, cf, cf, ci, vp, vp, cl, vp, cl, vp]),
     "ltq_ldlq_prep": (ci, [vp, cl, vp, cl, vp, cl, vp]),
     "ltq_ldlq_sub": (ci, [vp, cl, vp, vp, cl, vp, cl, vp, cl, ci, vp, cl, vp, cl, vp, vp, cl, vp, cl, vp]),
