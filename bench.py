@@ -1,19 +1,20 @@
 """Throughput of the TCQ Viterbi quantizer on one MI355X: the C3 headline workload.
 
 Workload (metric format TCQ275X2 = K=3 D4, 8 subsets, h=2): W [4096, 14336] bf16
-Student-t(5) * 0.02 with 143 outlier columns * 20, H = X^T X / 2048 from X [2048, 14336] N(0, 1), damping
-0.2 * mean(diag H_rot). The weight matrix is rotated (suh, FWHT-256), given its row scale (fp16 d_row +
-5-bit e per (row, 256-block)), and H is factored (U, diag_w) before the timed region, as inputs of the path.
+Student-t(5) * 0.02 with 143 outlier columns * 20, H = X^T X / 2048 from X [2048, 14336] N(0, 1) activations in
+bf16 (accumulated by ltq_cov_accumulate, the reference's _CovAccumulator, before the timed region and reported
+separately under `h_build`), damping 0.2 * mean(diag H_rot). W and H are resident in HBM when the timed region
+starts.
 
-One step quantizes the whole matrix the way src/liqk_v2.py:957-980 drives it: for each 256-column block and
-each 16-column sub-block, one two-pass tail-biting Viterbi over the 256 tiles of 16 rows x 16 columns
-(src/liqk_v2.py:917-919 -> src/tcq_proto.py:584-609), returning codes for PACK. All inputs are resident
-in HBM when the timed region starts.
+One step is quantize_matrix_liqk_v2 with PACK plus .ltq slice packing: rotation (suh, FWHT-256), factors of
+H_rot, row scale, and for each 256-column block and each 16-column sub-block one two-pass tail-biting Viterbi
+over the 256 tiles of 16 rows x 16 columns (src/liqk_v2.py:917-919 -> src/tcq_proto.py:584-609) with the LDLQ
+feedback, then the c_row / suh refit.
 
 Prints one JSON line (driver contract). `roofline` is the dominant kernel (the Viterbi) against the gfx950
-fp32 VALU peak, from HIP events recorded around every Viterbi pass inside the timed region on the stream
-the kernels run on; `cpu_baseline` is the C oracle (a scalar-per-thread port of the reference semantics,
-OpenMP over tiles) timed on this host on a bounded sample of the same workload.
+fp32 VALU peak, from HIP events recorded around every Viterbi pass of one sub-block in 16 inside the timed
+region, on the stream the kernels run on; `cpu_baseline` is the C oracle (a scalar-per-thread port of the
+reference semantics, OpenMP over tiles) timed on this host on a bounded sample of the same workload.
 """
 from __future__ import annotations
 
@@ -57,8 +58,33 @@ def prepare(dev, rows=M_ROWS, cols=K_COLS):
     W[:, cols_out.to(dev)] *= 20
     W = W.to(torch.bfloat16)
     X = torch.randn((N_ACT, cols), generator=torch.Generator(device=dev).manual_seed(1), device=dev)
-    H = (X.T @ X) / N_ACT
-    return W, H
+    H, h_build = build_hessian(X.to(torch.bfloat16))
+    return W, H, h_build
+
+
+def build_hessian(X):
+    """H = X^T X / n through CovAccumulator (one ltq_cov_accumulate + ltq_cov_finalize), timed with HIP events after
+    one untimed warm-up accumulation: the H-build figures reported beside the step."""
+    import torch
+    from ltq_amd.hessian import CovAccumulator
+    CovAccumulator().add(X)
+    stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    acc = CovAccumulator()
+    ev[0].record(stream)
+    acc.add(X)
+    ev[1].record(stream)
+    H = acc.get()
+    ev[2].record(stream)
+    torch.cuda.synchronize()
+    n, K = X.shape
+    nt = (K + 127) // 128
+    flop = 2.0 * n * 128 * 128 * nt * (nt + 1) // 2  # the lower-triangle 128 x 128 tiles the kernel computes
+    t_acc = ev[0].elapsed_time(ev[1]) * 1e-3
+    return H, {"rows": n, "cols": K, "dtype": "bf16", "accumulate_ms": round(t_acc * 1e3, 4),
+               "finalize_ms": round(ev[1].elapsed_time(ev[2]), 4), "mfma_tflops": round(flop / t_acc / 1e12, 1),
+               "frac_bf16_dense_peak": round(flop / t_acc / 2.5e15, 4),
+               "kernel": "ltq_cov_accumulate (cov_kernel<bf16>), fp32 MFMA accumulation into fp64 H"}
 
 
 def sample_tiles(W, H, nsub):
@@ -153,7 +179,7 @@ def main():
         torch.empty_like(a).copy_(a)
         torch.cuda.synchronize()
         del a
-    W, H = prepare(dev, cols=args.cols)
+    W, H, h_build = prepare(dev, cols=args.cols)
     rows, cols = W.shape
     stream = torch.cuda.current_stream()
 
@@ -215,7 +241,7 @@ def main():
         "value": round(value, 3), "unit": "Mweights/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic, generated on the device (Student-t(5)*0.02 bf16 weights, 143 outlier "
-                                "columns x20; H from 2048 N(0,1) rows; seeds 0/1/2)",
+                                "columns x20; H from 2048 N(0,1) bf16 activation rows; seeds 0/1/2)",
         "config": {"workload": f"C3 down_proj {rows}x{cols} {FORMAT} (K=3 D4, nl=8, h=2) tail-biting "
                                f"tb_window={TB_WINDOW}, damping {DAMP} mean(diag H_rot), LDLQ on: one step = "
                                f"quantize_matrix_liqk_v2 with PACK (rotation, factors, row scale, "
@@ -233,6 +259,7 @@ def main():
                       "viterbi_launches_per_step": n_launch, "viterbi_launches_timed": len(durs),
                       "proxy_rel_loss": round(rel, 6),
                       "packed_bytes": int(packed.numel())},
+        "h_build": h_build,
     }
     if args.cpu_seconds > 0:
         nsub = 16

@@ -85,30 +85,73 @@ def tri_inv_lower(L: torch.Tensor, leaf: int = 1024) -> torch.Tensor:
     return out
 
 
-def _solve_lower_vec(L: torch.Tensor, b: torch.Tensor, nb: int) -> torch.Tensor:
+def _diag_block_inverses(L: torch.Tensor, nb: int) -> list:
+    """Inverses of the nb x nb diagonal blocks of lower-triangular L (the last one ragged), full blocks in one
+    batched triangular solve."""
     n = L.shape[0]
-    x = torch.empty_like(b)
+    nfull = n // nb
+    out = []
+    if nfull:
+        blocks = torch.stack([L[i * nb:(i + 1) * nb, i * nb:(i + 1) * nb] for i in range(nfull)])
+        eye = torch.eye(nb, dtype=L.dtype, device=L.device).expand(nfull, nb, nb)
+        out = list(torch.linalg.solve_triangular(blocks, eye, upper=False).unbind(0))
+    if n % nb:
+        i = nfull * nb
+        out.append(torch.linalg.solve_triangular(L[i:, i:], torch.eye(n - i, dtype=L.dtype, device=L.device),
+                                                 upper=False))
+    return out
+
+
+def _solve_lower_vec(L: torch.Tensor, b: torch.Tensor, nb: int, Dinv=None) -> torch.Tensor:
+    """L x = b, right-looking by nb-row blocks: x_i = L_ii^-1 r_i, then r[j:] -= L[j:, i:j] x_i (a tall matrix-
+    vector product over the rows below the block)."""
+    n = L.shape[0]
+    Dinv = _diag_block_inverses(L, nb) if Dinv is None else Dinv
+    x = b.clone()
+    for k, i in enumerate(range(0, n, nb)):
+        j = min(n, i + nb)
+        x[i:j] = Dinv[k] @ x[i:j]
+        if j < n:
+            x[j:].addmv_(L[j:, i:j], x[i:j], alpha=-1.0)
+    return x
+
+
+def _solve_upper_vec(Ut: torch.Tensor, b: torch.Tensor, nb: int, Dinv=None) -> torch.Tensor:
+    """Ut x = b for Ut = L^T (upper), from the last block up: x_i = (L_ii^-1)^T r_i, then r[:i] -= L[i:j, :i]^T
+    x_i."""
+    L = Ut.T
+    n = L.shape[0]
+    Dinv = _diag_block_inverses(L, nb) if Dinv is None else Dinv
+    x = b.clone()
+    starts = list(range(0, n, nb))
+    for k in range(len(starts) - 1, -1, -1):
+        i = starts[k]
+        j = min(n, i + nb)
+        x[i:j] = Dinv[k].T @ x[i:j]
+        if i > 0:
+            x[:i].addmv_(L[i:j, :i].T, x[i:j], alpha=-1.0)
+    return x
+
+
+def gram_lower(A: torch.Tensor, B: torch.Tensor, nb: int = 2048) -> torch.Tensor:
+    """C = A^T B [n, n] for A, B [m, n] with C symmetric (B = diag(w) A or the like): only the block rows' parts
+    on and left of the diagonal are multiplied (A[:, I]^T B[:, :end of I]); the strict upper triangle of C beyond
+    them is zero."""
+    n = A.shape[1]
+    C = torch.zeros((n, n), dtype=A.dtype, device=A.device)
     for i in range(0, n, nb):
         j = min(n, i + nb)
-        r = b[i:j] - L[i:j, :i] @ x[:i] if i else b[i:j]
-        x[i:j] = torch.linalg.solve_triangular(L[i:j, i:j], r.unsqueeze(1), upper=False).squeeze(1)
-    return x
-
-
-def _solve_upper_vec(Ut: torch.Tensor, b: torch.Tensor, nb: int) -> torch.Tensor:
-    n = Ut.shape[0]
-    x = torch.empty_like(b)
-    for j in range(n, 0, -nb):
-        i = max(0, j - nb)
-        r = b[i:j] - Ut[i:j, j:] @ x[j:] if j < n else b[i:j]
-        x[i:j] = torch.linalg.solve_triangular(Ut[i:j, i:j], r.unsqueeze(1), upper=True).squeeze(1)
-    return x
+        C[i:j, :j] = A[:, i:j].T @ B[:, :j]
+    return C
 
 
 def spd_solve(A: torch.Tensor, b: torch.Tensor, nb: int = 512) -> torch.Tensor:
-    """x with A x = b for symmetric positive definite A [n, n], b [n]; LU solve when the Cholesky fails."""
+    """x with A x = b for symmetric positive definite A [n, n] (only its lower triangle is read), b [n]; LU solve
+    of the symmetric matrix when the Cholesky fails."""
     L, info = cholesky_lower(A)
     if int(info.item()) != 0:
-        return torch.linalg.solve(A, b)
-    y = _solve_lower_vec(L, b, nb)
-    return _solve_upper_vec(L.T, y, nb)
+        full = torch.tril(A) + torch.tril(A, -1).T
+        return torch.linalg.solve(full, b)
+    Dinv = _diag_block_inverses(L, nb)
+    y = _solve_lower_vec(L, b, nb, Dinv)
+    return _solve_upper_vec(L.T, y, nb, Dinv)

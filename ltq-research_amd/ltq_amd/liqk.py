@@ -245,7 +245,9 @@ def quantize_matrix_liqk_v2(W: torch.Tensor, H: torch.Tensor, spec_or_row_specs,
     else:
         rw = torch.ones((M,), dtype=torch.float32, device=W.device)
         U_w = U_scaled
-    A_in = (U_w.T @ U_scaled) * H_f32
+    # A_in = (U_w^T U_scaled) * H is symmetric (U_w = diag(rw) U_scaled): only its lower triangle is formed, which
+    # is all the Cholesky of spd_solve reads
+    A_in = linalg.gram_lower(U_w, U_scaled).mul_(H_f32)
     b_in = (U_w * HW).sum(dim=0)
     A_in.diagonal().add_(1e-3 * A_in.diagonal().mean().clamp(min=1e-12))
     try:
@@ -274,7 +276,15 @@ def quantize_matrix_liqk_v2(W: torch.Tensor, H: torch.Tensor, spec_or_row_specs,
         scale = d_row_p.float().unsqueeze(1) * torch.exp2(0.25 * pm["e"].float())
         Wq_rot = (scale.unsqueeze(2) * pm["G"].view(M, nblocks, QK_K)).view(M, K)
         W_hat_eff = rotation.fwht_inplace(Wq_rot, block_size=QK_K) * suh_p.float().unsqueeze(0)
-        HQ = W_hat_eff @ H_f32
+        # the rebuilt matrix is the refit's W_hat_eff with row r scaled by rho_r = d_row_p / (d_row c_pack) (same
+        # tile values, same fp16 suh), so its product with H is HQ scaled by row, equal to the reference's
+        # W_hat_eff @ H up to fp32 rounding; rows whose block scale hit the 1e-8 clamp of the row-scale fit (where
+        # the identity does not hold) are multiplied out
+        rho = d_row_p.float() / (pm["d_row"] * c_pack)
+        HQ = HQ * rho.unsqueeze(1)
+        clamped = ((pm["d_row"].unsqueeze(1) * torch.exp2(0.25 * pm["e"].float())) < 1e-8).any(dim=1)
+        if bool(clamped.any()):
+            HQ[clamped] = W_hat_eff[clamped] @ H_f32
         PACK["matrix"] = {"row_slices": row_slices, "idx": pm["idx"], "gi": pm["gi"], "G": pm["G"], "d_row": d_row_p,
                           "e": pm["e"], "suh": suh_p}
 

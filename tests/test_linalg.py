@@ -48,3 +48,30 @@ def test_spd_solve_falls_back_to_lu_for_indefinite():
 def test_blocked_linalg_gpu(n):
     print(f"blocked linalg n={n}", flush=True)
     _check(n, 2048 if n > 2304 else 512, 512, "cuda")
+
+
+@pytest.mark.parametrize("m,n,nb", [(50, 300, 64), (33, 257, 100)])
+def test_gram_lower_is_the_lower_triangle_of_the_product(m, n, nb):
+    from ltq_amd import linalg
+    g = torch.Generator().manual_seed(n)
+    A = torch.randn((m, n), generator=g, dtype=torch.float64)
+    B = A * torch.rand((m, 1), generator=g, dtype=torch.float64)  # diag(w) A: the product is symmetric
+    C = linalg.gram_lower(A, B, nb=nb)
+    full = A.T @ B
+    assert torch.allclose(torch.tril(C), torch.tril(full), rtol=1e-12, atol=1e-12)
+    # every block row is formed up to the end of its diagonal block, nothing to the right of it
+    for i in range(0, n, nb):
+        assert torch.all(C[i:i + nb, min(n, i + nb):] == 0)
+
+
+def test_spd_solve_reads_only_the_lower_triangle():
+    from ltq_amd import linalg
+    A = _spd(300, 5)
+    b = torch.randn(300, generator=torch.Generator().manual_seed(6))
+    junk = A + torch.triu(torch.full_like(A, 7.0), 1)
+    x = linalg.spd_solve(junk, b, nb=64).double()
+    xr = torch.linalg.solve(A.double(), b.double())
+    assert (x - xr).norm() <= 1e-5 * xr.norm()
+    # indefinite: the LU fallback rebuilds the symmetric matrix from the lower triangle
+    Ai = torch.tensor([[2.0, 99.0], [1.0, -1.0]])
+    assert torch.allclose(linalg.spd_solve(Ai, torch.tensor([3.0, 0.0])), torch.tensor([1.0, 1.0]))
