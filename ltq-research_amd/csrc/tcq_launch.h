@@ -34,6 +34,8 @@ struct GpuX {
     __device__ __forceinline__ float fmin(float x, float y) const { return __builtin_fminf(x, y); }
     __device__ __forceinline__ float shfl_xor(float v, int m) const { return __shfl_xor(v, m, 64); }
     __device__ __forceinline__ int shfl_xor(int v, int m) const { return __shfl_xor(v, m, 64); }
+    // instruction-scheduling barrier: nothing is moved across it (keeps loads issued ahead of the code they overlap)
+    __device__ __forceinline__ void sched_fence() const { __builtin_amdgcn_sched_barrier(0); }
     // a value every lane holds equally, pinned to a scalar register
     __device__ __forceinline__ int uni(int v) const { return __builtin_amdgcn_readfirstlane(v); }
     // acquire at device scope: drops this CU's L1 lines, so global data rewritten since it was last read (by

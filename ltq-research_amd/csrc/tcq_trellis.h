@@ -603,10 +603,11 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
     int next_merge = sub, merge_j = 1;   // next sub-block boundary and its index
     // chunk c; FIRST: chunk 0, whose phase 0 starts the trellis (compile-time, so no other phase carries the
     // start-state selects)
-    // streamlined traceback (whole chunks, one block per lane, a second wavefront, a ring of at least 3 chunks):
-    // the last chunk's decision words then go straight from registers to the traceback's LDS ring
+    // streamlined traceback (whole chunks, one block per lane, a second wavefront, a ring of at least 3 chunks,
+    // sub-blocks of 16 or 32): the last chunk's decision words then go straight from registers to the traceback's
+    // LDS ring
     bool fast = false;
-    if constexpr (RB == 2) fast = T % CK == 0 && nthr >= 128 && SM.nslot >= 3;
+    if constexpr (RB == 2) fast = T % CK == 0 && nthr >= 128 && SM.nslot >= 3 && (sub == 16 || sub == 32);
     uint32_t last_acc[NW];
 #pragma unroll
     for (int w = 0; w < NW; w++) last_acc[w] = 0;
@@ -785,9 +786,9 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
     // block; that lane's decision bits give the phase's input state, the intermediate state and the parity
     // classes. Lanes of the walking wavefront fetch the possible next lookups one phase ahead; v_readlane
     // picks the true one.
-    uint32_t* s_rec = (uint32_t*)s_st;  // per phase: output state | slot << 10 | e << 14 | classes << 15
-    // Streamlined walk (whole chunks, one block per lane, a second wavefront, a ring of at least 3 chunks;
-    // every matrix-path tile): wavefront 0 walks, wavefront 1 copies the decision words of the chunks ahead
+    uint16_t* s_rec = (uint16_t*)s_st;  // per phase: output state | slot << 10 | e << 13 | classes << 14
+    // Streamlined walk (whole chunks, one block per lane, a second wavefront, a ring of at least 3 chunks,
+    // sub-blocks of 16 or 32; every matrix-path tile): wavefront 0 walks, wavefront 1 copies the decision words of the chunks ahead
     // global -> LDS, one barrier per chunk hands them over, and every thread writes the outputs. Otherwise
     // wavefront 0 alone walks (copying its own words) and writes the outputs, and the others are done.
     if (!fast && wv != 0) return;
@@ -848,7 +849,6 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
             const int sxL = GE::start(hypL, 0, 0);
             const int wL = (sxL >> 8) & (Q - 1), lL = (sxL >> 2) & 63;
             int st = bi_all % S, gs = bi_all / S, cstar = 0;
-            int nbnd = ((T - 1) / sub) * sub, jb = (T - 1) / sub;
             uint32_t c0, c1, gv = 0;
             {  // exact words of the walk's first phase, in every lane
                 constexpr int P0 = MM::OFF(NPC - 1);
@@ -858,104 +858,149 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                 c1 = slot[wi + 64];
             }
             int sel = 0, mid_val = 0;
-            bool stop = false;
-            for (int k = 0; k < kmax; k++) {
-                const int cc = nchunk - 1 - k;
-                if (wv == 1) {  // chunk cc - nslot + 1 into the slot chunk cc + 1 left; chunk cc - 2 lands first
-                    if (cc - nslot + 1 >= 0) issue(cc - nslot + 1);
-                    X_.wait_loads(count(max_i(0, cc - nslot + 1), cc - 3) * nloads);
-                }
-                if (wv == 0) {
-                    const uint32_t* slot = ring + (cc % nslot) * slot_words;
-                    const uint32_t* slot_next = ring + ((cc + nslot - 1) % nslot) * slot_words;  // chunk cc - 1
-                    static_for<0, NPC>([&](auto Kc) {
-                        constexpr int pi = NPC - 1 - decltype(Kc)::value;
-                        constexpr int PT = MM::PT(pi);
-                        constexpr int P = MM::OFF(pi);
-                        constexpr int o = P - 32 * (P >> 5);
-                        constexpr int NB_ = MM::PBLK(PT);  // the phase's decision bits, first push highest
-                        constexpr bool TWO_WORDS = o + NB_ > 32;
-                        if (stop) return;
-                        const int ta = cc * CK + 2 * pi, ph = ta >> 1;
-                        const uint32_t W0 = X_.readlane(c0, sel);
-                        const uint32_t W1 = TWO_WORDS ? X_.readlane(c1, sel) : 0u;
-                        const bool bnd = G > 1 && ta == nbnd && ta > 0;
-                        const int qq = (st >> 8) & (Q - 1), ll = (st >> 2) & 63, jo = st & 3;
-                        // prefetch the words of the phase below for every hypothesis (and slot at a boundary), and
-                        // the merge choice of every hypothesis (an in-bounds byte even where it is not used)
-                        if (pi > 0 || cc > 0) {
-                            constexpr int PN = pi > 0 ? pi - 1 : NPC - 1;
-                            constexpr int PNw = MM::OFF(PN) >> 5;
-                            const int su = GE::start(0, qq, ll);
-                            const int gsl = bnd ? gp : gs;
-                            const int wi = ((gsl * Q + (((su >> 8) & (Q - 1)) | wL)) * NW + PNw) * 64 + (((su >> 2) & 63) | lL);
-                            const uint32_t* tsl = pi > 0 ? slot : slot_next;
-                            c0 = tsl[wi];
-                            c1 = tsl[wi + 64];
-                            gv = s_gsel[G > 1 ? jb * S + (su | sxL) : 0];
-                        }
-                        const uint32_t F = TWO_WORDS ? (uint32_t)(((((uint64_t)W0 << 32) | W1) >> (64 - o - NB_)) & ((1u << NB_) - 1u))
-                                                     : (W0 >> (32 - o - NB_)) & ((1u << NB_) - 1u);
-                        // n bits of F from position k on; the shift NB_ - k - n comes from tables indexed by jo
-                        auto fld = [&](int sh, int nbit) -> int { return (int)((F >> sh) & ((1u << nbit) - 1u)); };
-                        auto tab8 = [](uint32_t t, int i) -> int { return (int)((t >> (8 * i)) & 0xFFu); };
-                        int h = 0, e = 0, pa = 0, pb = 0;
-                        if constexpr (MD == 0) {  // e at 2 + ca, h at e
-                            e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 4) << 16) | ((NB_ - 4) << 24), jo), 1);
-                            h = fld(NB_ - 1 - e, 1);
-                        } else if constexpr (MD == 1) {  // p at 4 + 4 ca + cb, e at 2 + 4 ca + p, h at e
-                            const int p = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 6) << 8) | ((NB_ - 9) << 16) | ((NB_ - 10) << 24), jo), 1);
-                            e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 7) << 16) | ((NB_ - 7) << 24), jo) - p, 1);
-                            h = fld(NB_ - 1 - e, 1);
-                            pa = pb = p;
-                        } else if constexpr (!EQ) {
-                            if constexpr (PT == 1) {  // v3 at 8 + 10 ca + 3 cb (3 bits); e at 4 + 10 ca + idx; h at 2 e + c
-                                const int v3 = fld(tab8(((NB_ - 11) << 0) | ((NB_ - 14) << 8) | ((NB_ - 21) << 16) | ((NB_ - 24) << 24), jo), 3);
-                                const int idx = (0xEDEC >> (2 * v3)) & 3;
-                                cstar = idx >> 1;
-                                const int bsel = idx & 1;
-                                e = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 5) << 8) | ((NB_ - 15) << 16) | ((NB_ - 15) << 24), jo) - idx, 1);
-                                h = fld(NB_ - 1 - 2 * e - cstar, 1);
-                                pb = bsel ^ cstar;
-                                pa = bsel;
-                            } else {  // bsel at 4 + 6 ca + 2 cb + c; e at 2 + 6 ca + bsel; h at e
-                                const int bsel = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 7) << 8) | ((NB_ - 11) << 16) | ((NB_ - 13) << 24), jo) - cstar, 1);
-                                e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 9) << 16) | ((NB_ - 9) << 24), jo) - bsel, 1);
-                                h = fld(NB_ - 1 - e, 1);
-                                pb = bsel ^ cstar;
-                                pa = bsel;
+            const int lsub = sub == 16 ? 4 : 5;  // the fast walk serves sub 16 and 32
+            // word offset of this lane's hypothesis (wave and lane bits of start(hypL, 0, 0), disjoint from those of
+            // start(0, q, l)) in a ring slot, for the phases that cannot start a sub-block
+            const int lane_off = wL * NW * 64 + lL;
+            // The walk over chunks kmax .. : MIDW (first tail-biting pass) stops at the phase holding mid_t and writes
+            // no records; the full walk keeps every phase's 16-bit record in scalar registers and stores a chunk's
+            // records, two a word, at the end of the chunk. A sub-block can only start at a phase with 2 pi a
+            // multiple of 16 (sub is 16 or 32), so every other phase carries no boundary test, no merge-choice fetch
+            // and a scalar word address.
+            auto walk = [&](auto midw) {
+                constexpr bool MIDW = decltype(midw)::value;
+                bool stop = false;
+                for (int k = 0; k < kmax; k++) {
+                    const int cc = nchunk - 1 - k;
+                    if (wv == 1) {  // chunk cc - nslot + 1 into the slot chunk cc + 1 left; chunk cc - 2 lands first
+                        if (cc - nslot + 1 >= 0) issue(cc - nslot + 1);
+                        X_.wait_loads(count(max_i(0, cc - nslot + 1), cc - 3) * nloads);
+                    }
+                    if (wv == 0) {
+                        const uint32_t* slot = ring + (cc % nslot) * slot_words;
+                        const uint32_t* slot_next = ring + ((cc + nslot - 1) % nslot) * slot_words;  // chunk cc - 1
+                        uint32_t recs[NPC];
+                        static_for<0, NPC>([&](auto Kc) {
+                            constexpr int pi = NPC - 1 - decltype(Kc)::value;
+                            constexpr int PT = MM::PT(pi);
+                            constexpr int P = MM::OFF(pi);
+                            constexpr int o = P - 32 * (P >> 5);
+                            constexpr int NB_ = MM::PBLK(PT);  // the phase's decision bits, first push highest
+                            constexpr bool TWO_WORDS = o + NB_ > 32;
+                            constexpr bool BC = (2 * pi) % 16 == 0;
+                            if constexpr (MIDW) {
+                                if (stop) return;
                             }
-                        } else {
-                            if constexpr (PT == 1) {  // c at 6 + 4 ca + cb; e at 4 + 4 ca + c; h at 2 e + c
-                                cstar = fld(tab8(((NB_ - 7) << 0) | ((NB_ - 8) << 8) | ((NB_ - 11) << 16) | ((NB_ - 12) << 24), jo), 1);
-                                e = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 5) << 8) | ((NB_ - 9) << 16) | ((NB_ - 9) << 24), jo) - cstar, 1);
-                                h = fld(NB_ - 1 - 2 * e - cstar, 1);
-                            } else {  // e at 2 + 2 ca + c; h at e
-                                e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 5) << 16) | ((NB_ - 5) << 24), jo) - cstar, 1);
-                                h = fld(NB_ - 1 - e, 1);
+                            const int ta = cc * CK + 2 * pi, ph = ta >> 1;
+                            bool bnd = false;
+                            if constexpr (BC) bnd = G > 1 && ta > 0 && (ta & (sub - 1)) == 0;
+                            const int qq = (st >> 8) & (Q - 1), ll = (st >> 2) & 63, jo = st & 3;
+                            const uint32_t W0 = X_.readlane(c0, sel);
+                            const uint32_t W1 = TWO_WORDS ? X_.readlane(c1, sel) : 0u;
+                            X_.sched_fence();
+                            // prefetch the words of the phase below for every hypothesis (and, where a sub-block may
+                            // start, every slot, with the merge choice of every hypothesis: an in-bounds byte even
+                            // where it is not used). The addresses need only this phase's state: the loads go out
+                            // after this phase's words are read (so the wait for those does not cover them) and
+                            // before the decode, which they overlap; the fences keep the compiler from moving them.
+                            uint32_t n0 = c0, n1 = c1;
+                            if (pi > 0 || cc > 0) {
+                                constexpr int PN = pi > 0 ? pi - 1 : NPC - 1;
+                                constexpr int PNw = MM::OFF(PN) >> 5;
+                                const int su = GE::start(0, qq, ll);
+                                const uint32_t* tsl = pi > 0 ? slot : slot_next;
+                                if constexpr (BC) {
+                                    const int gsl = bnd ? gp : gs;
+                                    const int wi = ((gsl * Q + (((su >> 8) & (Q - 1)) | wL)) * NW + PNw) * 64 + (((su >> 2) & 63) | lL);
+                                    n0 = tsl[wi];
+                                    n1 = tsl[wi + 64];
+                                    gv = s_gsel[G > 1 ? (ta >> lsub) * S + (su | sxL) : 0];
+                                } else {
+                                    const uint32_t* tb = tsl + X_.uni(((gs * Q + ((su >> 8) & (Q - 1))) * NW + PNw) * 64 + ((su >> 2) & 63));
+                                    n0 = tb[lane_off];
+                                    n1 = tb[lane_off + 64];
+                                }
                             }
-                            pa = pb = cstar;
+                            X_.sched_fence();
+                            c0 = n0;
+                            c1 = n1;
+                            const uint32_t F = TWO_WORDS ? (uint32_t)(((((uint64_t)W0 << 32) | W1) >> (64 - o - NB_)) & ((1u << NB_) - 1u))
+                                                         : (W0 >> (32 - o - NB_)) & ((1u << NB_) - 1u);
+                            // n bits of F from position k on; the shift NB_ - k - n comes from tables indexed by jo
+                            auto fld = [&](int sh, int nbit) -> int { return (int)((F >> sh) & ((1u << nbit) - 1u)); };
+                            auto tab8 = [](uint32_t t, int i) -> int { return (int)((t >> (8 * i)) & 0xFFu); };
+                            int h = 0, e = 0, pa = 0, pb = 0;
+                            if constexpr (MD == 0) {  // e at 2 + ca, h at e
+                                e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 4) << 16) | ((NB_ - 4) << 24), jo), 1);
+                                h = fld(NB_ - 1 - e, 1);
+                            } else if constexpr (MD == 1) {  // p at 4 + 4 ca + cb, e at 2 + 4 ca + p, h at e
+                                const int p = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 6) << 8) | ((NB_ - 9) << 16) | ((NB_ - 10) << 24), jo), 1);
+                                e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 7) << 16) | ((NB_ - 7) << 24), jo) - p, 1);
+                                h = fld(NB_ - 1 - e, 1);
+                                pa = pb = p;
+                            } else if constexpr (!EQ) {
+                                if constexpr (PT == 1) {  // v3 at 8 + 10 ca + 3 cb (3 bits); e at 4 + 10 ca + idx; h at 2 e + c
+                                    const int v3 = fld(tab8(((NB_ - 11) << 0) | ((NB_ - 14) << 8) | ((NB_ - 21) << 16) | ((NB_ - 24) << 24), jo), 3);
+                                    const int idx = (0xEDEC >> (2 * v3)) & 3;
+                                    cstar = idx >> 1;
+                                    const int bsel = idx & 1;
+                                    e = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 5) << 8) | ((NB_ - 15) << 16) | ((NB_ - 15) << 24), jo) - idx, 1);
+                                    h = fld(NB_ - 1 - 2 * e - cstar, 1);
+                                    pb = bsel ^ cstar;
+                                    pa = bsel;
+                                } else {  // bsel at 4 + 6 ca + 2 cb + c; e at 2 + 6 ca + bsel; h at e
+                                    const int bsel = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 7) << 8) | ((NB_ - 11) << 16) | ((NB_ - 13) << 24), jo) - cstar, 1);
+                                    e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 9) << 16) | ((NB_ - 9) << 24), jo) - bsel, 1);
+                                    h = fld(NB_ - 1 - e, 1);
+                                    pb = bsel ^ cstar;
+                                    pa = bsel;
+                                }
+                            } else {
+                                if constexpr (PT == 1) {  // c at 6 + 4 ca + cb; e at 4 + 4 ca + c; h at 2 e + c
+                                    cstar = fld(tab8(((NB_ - 7) << 0) | ((NB_ - 8) << 8) | ((NB_ - 11) << 16) | ((NB_ - 12) << 24), jo), 1);
+                                    e = fld(tab8(((NB_ - 5) << 0) | ((NB_ - 5) << 8) | ((NB_ - 9) << 16) | ((NB_ - 9) << 24), jo) - cstar, 1);
+                                    h = fld(NB_ - 1 - 2 * e - cstar, 1);
+                                } else {  // e at 2 + 2 ca + c; h at e
+                                    e = fld(tab8(((NB_ - 3) << 0) | ((NB_ - 3) << 8) | ((NB_ - 5) << 16) | ((NB_ - 5) << 24), jo) - cstar, 1);
+                                    h = fld(NB_ - 1 - e, 1);
+                                }
+                                pa = pb = cstar;
+                            }
+                            if constexpr (MIDW) {
+                                if (ph == mid_ph) {  // first tail-biting pass: only the state before mid_t is needed
+                                    mid_val = (a.mid_t - 1) & 1 ? st : GE::mid(0, 2 * (jo >> 1) + e, qq, ll);
+                                    stop = true;
+                                    return;
+                                }
+                            } else {
+                                recs[pi] = (uint32_t)(st | (gs << 10) | (e << 13) | (pa << 14) | (pb << 15));
+                            }
+                            const int Ln = X_.uni(2 * h + e);
+                            st = X_.uni(GE::start(Ln, qq, ll));  // state at step ta - 1
+                            sel = Ln;
+                            cstar = X_.uni(cstar);
+                            if (bnd) {  // sub-block start: the path came from the slot the merge chose
+                                gs = (int)X_.readlane(gv, Ln);
+                                sel = Ln + 4 * gs;
+                            }
+                        });
+                        if constexpr (!MIDW) {
+                            if (lane == 0) {
+                                uint32_t* dst = (uint32_t*)s_rec + cc * (NPC / 2);
+                                static_for<0, NPC / 2>([&](auto Wc) {
+                                    constexpr int w = decltype(Wc)::value;
+                                    dst[w] = recs[2 * w] | (recs[2 * w + 1] << 16);
+                                });
+                            }
                         }
-                        s_rec[ph] = (uint32_t)(st | (gs << 10) | (e << 14) | (pa << 15) | (pb << 16));
-                        if (ph == mid_ph) {  // first tail-biting pass: only the state before mid_t is needed
-                            mid_val = (a.mid_t - 1) & 1 ? st : GE::mid(0, 2 * (jo >> 1) + e, qq, ll);
-                            stop = true;
-                            return;
-                        }
-                        const int Ln = X_.uni(2 * h + e);
-                        st = X_.uni(GE::start(Ln, qq, ll));  // state at step ta - 1
-                        sel = Ln;
-                        cstar = X_.uni(cstar);
-                        if (bnd) {  // sub-block start: the path came from the slot the merge chose
-                            gs = (int)X_.readlane(gv, Ln);
-                            sel = Ln + 4 * gs;
-                            nbnd -= sub;
-                            jb--;
-                        }
-                    });
+                    }
+                    X_.lds_sync();  // the records of chunk cc are written; chunk cc - 2 is in LDS; slot of cc + 1 free
                 }
-                X_.lds_sync();  // the records of chunk cc are written; chunk cc - 2 is in LDS; slot of cc + 1 free
-            }
+            };
+            if (a.mid_st)
+                walk(std::true_type{});
+            else
+                walk(std::false_type{});
             if (wv == 1) X_.wait_loads(0);  // no copy may still land in this workgroup's LDS after it ends
             if (wv == 0 && lane == 0) {
                 if (a.mid_st) a.mid_st[n] = mid_val;
@@ -1077,7 +1122,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                 }
                 const int ph = ta >> 1;
                 // the phase's output state, slot, intermediate bit and classes (the step-ta state follows from them)
-                s_rec[ph] = (uint32_t)(st | (gs << 10) | (e << 14) | (pa << 15) | (pb << 16));
+                s_rec[ph] = (uint16_t)(st | (gs << 10) | (e << 13) | (pa << 14) | (pb << 15));
                 if (ph == mid_ph) {  // first tail-biting pass: only the state before mid_t is needed
                     if (lane == 0) a.mid_st[n] = (a.mid_t - 1) & 1 ? st : GE::mid(bb, 2 * ca + e, qq, ll);
                     done = true;
@@ -1110,12 +1155,12 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
     float* rn = a.rec + (size_t)n * a.ld;
     for (int t = out_t0; t < T; t += out_dt) {
         const uint32_t rr = s_rec[t >> 1];
-        const int so = rr & 1023, gg = (rr >> 10) & 15;
+        const int so = rr & 1023, gg = (rr >> 10) & 7;
         // odd step: the phase's output state; even step: its intermediate state (block bits, e, ca, q, lane of so)
         const int stt = (t & 1) ? so
-                                : GE::mid(so >> (8 + QB), 2 * ((so >> 1) & 1) + ((rr >> 14) & 1), (so >> 8) & (Q - 1),
+                                : GE::mid(so >> (8 + QB), 2 * ((so >> 1) & 1) + ((rr >> 13) & 1), (so >> 8) & (Q - 1),
                                           (so >> 2) & 63);
-        const int par = (rr >> ((t & 1) ? 16 : 15)) & 1;
+        const int par = (rr >> ((t & 1) ? 15 : 14)) & 1;
         const int lb = mk.label(stt);
         const bool hi = mix > 0 && ((t / mix) & 1);
         const int Ut = hi ? U_hi : U;

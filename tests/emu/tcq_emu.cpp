@@ -62,6 +62,7 @@ struct CpuX {
     int uni(int v) const { return v; }
     int load_coherent(const int* p) const { return *p; }
     void acquire() const {}
+    void sched_fence() const {}
     uint32_t readlane(uint32_t v, int l) const
     {
         const int w = tid_ >> 6;

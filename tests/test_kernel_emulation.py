@@ -38,6 +38,10 @@ CASES = [
     dict(pp=2, ext=(40, 475, 211), G=2, T=32),
     dict(pp=0, ext=(40, 475, 211), G=4, T=32, n_cand=4, Gfull=8),
     dict(pp=0, ext=(), G=1, T=64, S=256, mid_t=33),
+    # sub-blocks of 32 through the streamlined walk (a merge at every other chunk), also with a mid-state pass
+    dict(pp=0, ext=(241,), G=2, T=64, sub=32),
+    dict(pp=1, ext=(241,), G=4, T=64, sub=32, mid_t=40),
+    dict(pp=2, ext=(241,), G=2, T=96, sub=32, init=True, tail=True),
 ]
 
 
