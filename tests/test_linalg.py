@@ -21,6 +21,10 @@ def _check(n, leaf, nb, device):
     Lr = torch.linalg.cholesky(A.double().cpu())
     Lc = L.double().cpu()
     assert torch.equal(Lc, torch.tril(Lc))
+    # backward error of a float32 Cholesky (of the order of sqrt(n) u |A| for any order of the sums; a wrong
+    # update or solve gives O(|A|)), then the forward error against LAPACK in float64
+    Ad = A.double().cpu()
+    assert (Lc @ Lc.T - Ad).abs().max() <= 1e-5 * Ad.abs().max()
     assert (Lc - Lr).abs().max() <= 2e-6 * Lr.abs().max()
     Li = linalg.tri_inv_lower(L, leaf=leaf).double().cpu()
     assert torch.equal(Li, torch.tril(Li))
