@@ -7,8 +7,9 @@
                    L21 = A21 L11^-T (trsm), L22 = chol(A22 - L21 L21^T), leaves to torch.linalg.cholesky_ex.
                    Used for src/liqk_v2.py:1079 (the flipped, damped Hessian) and for the SPD system of the
                    suh refit (src/liqk_v2.py:1163).
-  tri_inv_lower    L^-1 for lower-triangular L, recursive: [[A, 0], [B, C]]^-1 = [[A^-1, 0], [-C^-1 B A^-1, C^-1]].
-                   Replaces solve_triangular(L, I) (src/liqk_v2.py:1081) at a third of the flops.
+  tri_inv_lower    L^-1 for lower-triangular L, recursive: [[A, 0], [B, C]]^-1 = [[A^-1, 0], [-C^-1 B A^-1, C^-1]],
+                   the two products with triangular factors themselves recursive (n^3 / 3 flops in all).
+                   Replaces solve_triangular(L, I) (src/liqk_v2.py:1081).
   spd_solve        A x = b through cholesky_lower and two blocked substitutions; falls back to the LU solve
                    of src/liqk_v2.py:1163 when A is not numerically positive definite.
 
@@ -70,8 +71,36 @@ def cholesky_lower(A: torch.Tensor, leaf: int = 2048, magma: bool = True) -> Tup
     return L, i1.abs() + i2.abs()
 
 
+def _trmm_right_lower(B: torch.Tensor, T: torch.Tensor, out: torch.Tensor, leaf: int) -> None:
+    """out = B T for lower-triangular T [h, h] (strict upper triangle zero), B [m, h]:
+    [B1 B2] [[T11, 0], [T21, T22]] = [B1 T11 + B2 T21, B2 T22], recursively, so the zero triangle costs no flops
+    above the leaf size."""
+    h = T.shape[0]
+    if h <= leaf:
+        out.addmm_(B, T, beta=0.0)
+        return
+    s = _split(h)
+    _trmm_right_lower(B[:, :s], T[:s, :s], out[:, :s], leaf)
+    out[:, :s].addmm_(B[:, s:], T[s:, :s])
+    _trmm_right_lower(B[:, s:], T[s:, s:], out[:, s:], leaf)
+
+
+def _trmm_left_lower(T: torch.Tensor, B: torch.Tensor, out: torch.Tensor, leaf: int) -> None:
+    """out = T B for lower-triangular T [h, h], B [h, m]: [[T11, 0], [T21, T22]] [B1; B2] = [T11 B1; T21 B1 + T22 B2]."""
+    h = T.shape[0]
+    if h <= leaf:
+        out.addmm_(T, B, beta=0.0)
+        return
+    s = _split(h)
+    _trmm_left_lower(T[:s, :s], B[:s], out[:s], leaf)
+    _trmm_left_lower(T[s:, s:], B[s:], out[s:], leaf)
+    out[s:].addmm_(T[s:, :s], B[:s])
+
+
 def tri_inv_lower(L: torch.Tensor, leaf: int = 1024) -> torch.Tensor:
-    """Inverse of a lower-triangular matrix (its strict upper triangle must be zero)."""
+    """Inverse of a lower-triangular matrix (its strict upper triangle must be zero). The off-diagonal block
+    -C^-1 (B A^-1) is two triangular-times-full products, each done recursively on the triangle (half the flops of
+    full GEMMs)."""
     n = L.shape[0]
     if n <= leaf:
         return torch.linalg.solve_triangular(L, torch.eye(n, dtype=L.dtype, device=L.device), upper=False)
@@ -81,7 +110,11 @@ def tri_inv_lower(L: torch.Tensor, leaf: int = 1024) -> torch.Tensor:
     Ci = tri_inv_lower(L[h:, h:], leaf)
     out[:h, :h] = Ai
     out[h:, h:] = Ci
-    out[h:, :h] = -(Ci @ (L[h:, :h] @ Ai))
+    BA = torch.empty((n - h, h), dtype=L.dtype, device=L.device)
+    _trmm_right_lower(L[h:, :h], Ai, BA, leaf)
+    CBA = torch.empty_like(BA)
+    _trmm_left_lower(Ci, BA, CBA, leaf)
+    out[h:, :h] = CBA.neg_()
     return out
 
 

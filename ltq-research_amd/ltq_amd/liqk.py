@@ -58,11 +58,13 @@ def factor_hessian(H_rot: torch.Tensor, damp: float) -> Tuple[torch.Tensor, torc
     if int(info.item()) != 0:
         raise torch.linalg.LinAlgError("factor_hessian: the damped Hessian is not positive definite")
     U = linalg.tri_inv_lower(L_flip).flip(0, 1).contiguous()  # the kernels take row-major factors
-    del L_flip
     diag_w = 1.0 / (torch.diagonal(U) ** 2).clamp(min=1e-12)
-    eye = torch.eye(QK_K, dtype=torch.float32, device=H_rot.device).unsqueeze(0).expand(nblocks, -1, -1)
-    U_blks = torch.stack([U[b * QK_K:(b + 1) * QK_K, b * QK_K:(b + 1) * QK_K] for b in range(nblocks)], dim=0)
-    U_blks_inv = torch.linalg.solve_triangular(U_blks, eye, upper=True).contiguous()
+    # U = J L'^-1 J (J reverses the order), so U's diagonal block b is J (L'_cc)^-1 J with c = nblocks - 1 - b
+    # and its inverse is J L'_cc J: the flipped diagonal blocks of the factor (src/liqk_v2.py:1086-1088 inverts
+    # them numerically)
+    U_blks_inv = torch.stack([L_flip[c * QK_K:(c + 1) * QK_K, c * QK_K:(c + 1) * QK_K]
+                              for c in range(nblocks - 1, -1, -1)]).flip(1, 2).contiguous()
+    del L_flip
     return U, diag_w, U_blks_inv
 
 
