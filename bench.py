@@ -148,6 +148,95 @@ def cpu_baseline(tiles, wts, budget_s):
                       f"the Viterbi stage only, to compare with breakdown.mweights_s_viterbi"}
 
 
+C5_ROWS, C5_COLS = 262144, 2560  # K=4 D4 rings = TCQ375X; TCQ4X on request
+RING_SCALES = 3  # quantize_rings' scale candidates (src/ple_quant.py:53)
+# ring mode TCQ4X:rot (3 scales x 2 passes), 2.82e9 values in 33.18 s = 84.9 Mvalues/s (GPU unstated)
+RING_PUBLISHED = {"TCQ4X": 84.9}
+
+
+def prepare_rings(dev, rows):
+    """C5 table [rows, 2560] bf16: N(0, 0.02^2) times a per-row log-normal(0, 0.5) norm (seeds 0 and 1)."""
+    import torch
+    W = torch.randn((rows, C5_COLS), generator=torch.Generator(device=dev).manual_seed(0), device=dev) * 0.02
+    s = torch.exp(0.5 * torch.randn((rows, 1), generator=torch.Generator(device=dev).manual_seed(1), device=dev))
+    return (W * s).to(torch.bfloat16)
+
+
+def cpu_baseline_rings(W_sample, budget_s, fmt_name):
+    """oracle/ple_ref.py (the ring quantizer over the C oracle Viterbi, OpenMP over rings) on a few rows, cycled
+    until budget_s is spent."""
+    from oracle import ple_ref, ref
+    from ltq_amd.formats import TCQ_CONFIG, make_format
+    ref.lib()
+    cfg, fmt = TCQ_CONFIG[fmt_name], make_format(fmt_name)
+    cores = min(16, len(os.sched_getaffinity(0)))
+    done, k, t0 = 0, 0, time.perf_counter()
+    while time.perf_counter() - t0 <= budget_s:
+        row = W_sample[k % W_sample.shape[0]:k % W_sample.shape[0] + 1]
+        ple_ref.quantize_rings_ref(row, cfg, fmt, rot=True)
+        done += row.numel()
+        k += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(done / dt / 1e6, 5), "unit": "Mvalues/s", "cores": cores, "kind": "port",
+            "sample": f"oracle/ple_ref.py quantize_rings_ref (3 scales, two-pass tail-biting Viterbi of the C oracle) "
+                      f"on {k} rows of 2560 values ({done} values) cycling over {W_sample.shape[0]} rows of the table, "
+                      f"{dt:.1f} s on up to {cores} OpenMP threads"}
+
+
+def run_rings(args):
+    """--workload c5: one step = quantize_rings_packed over the whole C5 table (ring rotation, 3 fp16 scales x
+    two-pass tail-biting Viterbi per ring, selection, ring records)."""
+    import torch
+    from ltq_amd import ple_quant, tcq_proto
+    from ltq_amd.formats import TCQ_CONFIG
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    rows = args.rows or C5_ROWS
+    W = prepare_rings(dev, rows)
+    fmt_name = args.format or "TCQ375X"
+    step = lambda: ple_quant.quantize_rings_packed(W, fmt_name, rot=True)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    tcq_proto.LAUNCH_EVENTS, tcq_proto.LAUNCH_SAMPLE, tcq_proto._launch_count = [], 1, 0
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    evs, tcq_proto.LAUNCH_EVENTS = tcq_proto.LAUNCH_EVENTS, None
+    t_vit = sum(a.elapsed_time(b) for a, b in evs) * 1e-3 / args.steps
+    cfg = TCQ_CONFIG[fmt_name]
+    nl = 4 << len(cfg.get("m_extra", ()))
+    n_rings = W.numel() // 256
+    ops = n_rings * RING_SCALES * 2 * 256 * LANE_OPS_PER_STEP[int(cfg.get("pp", 0))] * 1024 * (cfg.get("n_cand", 0) or (1 << cfg["h"]))
+    achieved = ops / t_vit / 1e12
+    value = W.numel() / (dt / args.steps) / 1e6
+    pub = RING_PUBLISHED.get(fmt_name)
+    res = {
+        "metric": f"Mvalues/s quantized rings ({fmt_name}, 3 scales x 2 passes, {rows}x{C5_COLS} row table) on 1 GPU; "
+                  f"% VALU ACS roofline",
+        "value": round(value, 3), "unit": "Mvalues/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": round(value / pub, 3) if pub else None,
+        "dtype": "f32",
+        "data": "synthetic, generated on the device (N(0, 0.02^2) x per-row log-normal(0, 0.5) norm, bf16; seeds 0/1)",
+        "config": {"workload": f"C5 row table {rows}x{C5_COLS} {fmt_name} rings: FWHT-256 per ring, 3 fp16 scales "
+                               f"x two-pass tail-biting Viterbi (tb_window 0), selection, ring records",
+                   "format": fmt_name, "rows": rows, "cols": C5_COLS, "parallelism": "single GPU"},
+        "roofline": {"bound": "valu", "timed_on": "HIP events around every Viterbi launch of the timed steps",
+                     "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
+                     "unit": "TFLOP/s (fp32 VALU lane-ops/s x 1e-12)", "frac": round(achieved / VALU_PEAK_TOPS, 4),
+                     "traffic": None, "kernel": f"tcq_viterbi_kernel<10,2,{int(cfg.get('pp', 0))},{nl}>",
+                     "viterbi_ms_per_step": round(t_vit * 1e3, 2),
+                     "viterbi_launches_per_step": len(evs) // args.steps},
+        "breakdown": {"mvalues_s_viterbi": round(W.numel() / t_vit / 1e6, 3), "bits_per_value": out[1]},
+    }
+    if args.cpu_seconds > 0:
+        res["cpu_baseline"] = cpu_baseline_rings(W[:64].float().cpu(), args.cpu_seconds, fmt_name)
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -158,6 +247,10 @@ def main():
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="profiling runs: first copy this many MiB device-to-device (a known-size kernel that "
                          "calibrates the FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--workload", choices=("c3", "c5"), default="c3",
+                    help="c3: the headline matrix quantizer (default); c5: the ring table (an extra line on request)")
+    ap.add_argument("--rows", type=int, default=0, help="c5: table rows (default 262144)")
+    ap.add_argument("--format", default="", help="c5: ring format (default TCQ375X, K=4 D4; TCQ4X as published)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the quantizer is row-sharded with no exchange on the hot path, "
@@ -165,6 +258,8 @@ def main():
         sys.exit(2)
     if args.cols % 256 or args.cols <= 0:
         sys.exit("--cols must be a positive multiple of 256")
+    if args.workload == "c5":
+        return run_rings(args)
 
     import torch
     from ltq_amd import liqk, ltq_file, tcq_proto

@@ -75,15 +75,19 @@ struct GpuX {
     }
 };
 
-// Up to 16 wavefronts (1024 threads): G gain slots x Q waves.
-template <int NU, int RB, int MD, int NL>
-__global__ __launch_bounds__(1024) void tcq_viterbi_kernel(TcqArgs a, int lds_max)
+// Up to 16 wavefronts (1024 threads): G gain slots x Q waves. WMIN = 8 (waves per SIMD) builds the integer-mode
+// instance for two workgroups per CU (64 VGPRs), used with half the LDS when a launch has at least two tiles per
+// CU: its phases are bound by barrier and LDS latency rather than VALU, which a second workgroup overlaps
+// (ring tables); with one tile per CU the 83-VGPR build (WMIN = 1) is faster.
+template <int NU, int RB, int MD, int NL, int WMIN = 1>
+__global__ __launch_bounds__(1024, WMIN) void tcq_viterbi_kernel(TcqArgs a, int lds_max)
 {
     GpuX x;
     tcq_tile<NU, RB, MD, NL>(a, x, lds_max);
 }
 
 int device_lds_max();
+int device_cu_count();
 
 // Both tail-biting passes of every tile in one launch.
 template <int NU, int RB, int MD, int NL>
@@ -98,6 +102,23 @@ int launch(const TcqArgs& a, hipStream_t stream)
 {
     const int lds_max = device_lds_max();
     if (lds_max <= 0) return -1;
+    if constexpr (MD == 0 && RB == 2) {
+        const int cus = device_cu_count();
+        const int half = lds_max / 2;
+        const Smem H = smem_layout<NU, RB, MD, NL>(a.T, a.G, a.Gfull, a.sub, half);
+        if (cus > 0 && a.N >= 2 * cus && H.total <= half) {
+            static bool attr2 = false;
+            if (!attr2) {
+                (void)hipFuncSetAttribute((const void*)tcq_viterbi_kernel<NU, RB, MD, NL, 8>,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, half);
+                attr2 = true;
+            }
+            const int threads = 64 * a.G * Geo<NU, RB>::Q;
+            hipLaunchKernelGGL((tcq_viterbi_kernel<NU, RB, MD, NL, 8>), dim3(a.N), dim3(threads), H.total, stream, a,
+                               half);
+            return 0;
+        }
+    }
     const Smem L = smem_layout<NU, RB, MD, NL>(a.T, a.G, a.Gfull, a.sub, lds_max);
     if (L.total > lds_max) return -1;
     static bool attr = false;

@@ -38,6 +38,18 @@ int device_lds_max()
     return v;
 }
 
+int device_cu_count()
+{
+    static int v = -1;
+    if (v < 0) {
+        int dev = 0, x = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return -1;
+        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
+        v = x;
+    }
+    return v;
+}
+
 struct GpuLaunch {
     const TcqArgs& a;
     hipStream_t st;

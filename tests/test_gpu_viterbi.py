@@ -163,6 +163,32 @@ def test_tail_biting_driver_matches_oracle(tp, oracle, name, tb_window):
     assert np.array_equal(_u32(rec.cpu().numpy()), _u32(r_rec))
 
 
+@pytest.mark.parametrize("name,tb_window", [("TCQ4X", 0), ("TCQ2X", 32), ("TCQ3X3", 0)])
+def test_integer_launch_with_two_workgroups_per_cu_matches_oracle(tp, oracle, name, tb_window):
+    """Integer-mode launches with at least two tiles per CU run the two-workgroups-per-CU build of the kernel
+    (half the LDS, 64 VGPRs): bit-exact against the oracle like the one-workgroup build."""
+    from ltq_amd.formats import TCQ_CONFIG, make_format
+    cfg, f = TCQ_CONFIG[name], make_format(name)
+    N = 2 * torch.cuda.get_device_properties(0).multi_processor_count + 37
+    rng = np.random.default_rng(11)
+    x = (rng.standard_t(5, size=(N, 256)) * 0.9).astype(np.float32)
+    wts = np.tile((rng.random(16) * 2 + 0.2).astype(np.float32), 16)
+    n_cand = cfg.get("n_cand", 0)
+    print(f"two workgroups per CU: {name} N={N} window {tb_window}", flush=True)
+    rec, gi, idx = tp.viterbi_ub_cuda(torch.tensor(x, device=DEV), torch.tensor(f.lut, device=DEV), f.K, 10, 359,
+                                      torch.tensor(f.gain_tab, device=DEV), sub=f.sub, wts=torch.tensor(wts, device=DEV),
+                                      n_cand=n_cand, tail_biting=True, tb_window=tb_window, m_extra=f.masks[1:],
+                                      pair_parity=int(cfg.get("pp", 0)), return_code=True)
+    torch.cuda.synchronize()
+    r_rec, r_gi, r_idx = oracle.viterbi_ub_cuda_ref(x, f.lut, f.K, 10, 359, f.gain_tab, sub=f.sub, wts=wts,
+                                                    n_cand=n_cand, tail_biting=True, tb_window=tb_window,
+                                                    m_extra=f.masks[1:], pair_parity=int(cfg.get("pp", 0)),
+                                                    return_code=True)
+    assert np.array_equal(gi.cpu().numpy(), r_gi)
+    assert np.array_equal(idx.cpu().numpy(), r_idx)
+    assert np.array_equal(_u32(rec.cpu().numpy()), _u32(r_rec))
+
+
 def test_rejected_configs_raise(tp):
     x = torch.zeros((2, 32), device=DEV)
     with pytest.raises(RuntimeError):
