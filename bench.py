@@ -227,7 +227,7 @@ def run_rings(args):
         "roofline": {"bound": "valu", "timed_on": "HIP events around every Viterbi launch of the timed steps",
                      "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
                      "unit": "TFLOP/s (fp32 VALU lane-ops/s x 1e-12)", "frac": round(achieved / VALU_PEAK_TOPS, 4),
-                     "traffic": None, "kernel": f"tcq_viterbi_kernel<10,2,{int(cfg.get('pp', 0))},{nl}>",
+                     "traffic": None, "kernel": f"tcq_viterbi_kernel<10,2,{int(cfg.get('pp', 0))},{nl},{8 if int(cfg.get('pp', 0)) == 0 else 1}>",
                      "viterbi_ms_per_step": round(t_vit * 1e3, 2),
                      "viterbi_launches_per_step": len(evs) // args.steps},
         "breakdown": {"mvalues_s_viterbi": round(W.numel() / t_vit / 1e6, 3), "bits_per_value": out[1]},
@@ -345,7 +345,7 @@ def main():
                    "format": FORMAT, "rows": rows, "cols": cols, "parallelism": "single GPU"},
         "roofline": {"bound": "valu", "timed_on": "HIP events around both passes of one sub-block in 16", "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
                      "unit": "TFLOP/s (fp32 VALU lane-ops/s x 1e-12)", "frac": round(achieved / VALU_PEAK_TOPS, 4),
-                     "traffic": traffic, "kernel": "tcq_viterbi_kernel<10,2,2,8>",
+                     "traffic": traffic, "kernel": "tcq_viterbi_kernel<10,2,2,8,1>",
                      "avg_launch_us": round(avg * 1e6, 2), "pass1_us": round(t_p1 * 1e6, 2),
                      "pass2_us": round(t_p2 * 1e6, 2), "lane_ops_per_launch": ops},
         "breakdown": {"stages_ms": {k: round(v, 3) for k, v in stages.items()},

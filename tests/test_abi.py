@@ -49,3 +49,27 @@ def test_product_path_fails_loudly_without_device():
         fwht_rows(torch.zeros((1, 256)))
     with pytest.raises(_lib.LtqLibraryMissing):
         viterbi_ub_cuda(torch.zeros((1, 32)), torch.zeros(16), 3, 10, 359)
+
+
+def test_hessian_entry_points_reject_bad_arguments_without_a_device():
+    """ltq_cov_accumulate / ltq_cov_finalize validate their arguments before any device call (-1)."""
+    from ltq_amd import _lib
+    so = ROOT / "ltq-research_amd" / "ltq_amd" / "libltq_hip.so"
+    if not so.exists():
+        pytest.skip("libltq_hip.so not built (run __graft_entry__.build())")
+    L = ctypes.CDLL(str(so))
+    for name, (res, args) in _lib.SIGNATURES.items():
+        if name.startswith("ltq_cov"):
+            getattr(L, name).restype, getattr(L, name).argtypes = res, args
+    buf = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation first
+    acc, fin = L.ltq_cov_accumulate, L.ltq_cov_finalize
+    assert acc(buf, -1, 8, 8, 0, buf, 8, None) == -1     # negative rows
+    assert acc(buf, 4, 0, 8, 0, buf, 8, None) == -1      # K < 1
+    assert acc(buf, 4, 8, 7, 0, buf, 8, None) == -1      # ldx < K
+    assert acc(buf, 4, 8, 8, 2, buf, 8, None) == -1      # element type flag
+    assert acc(buf, 4, 8, 8, 0, None, 8, None) == -1     # no H
+    assert acc(None, 4, 8, 8, 0, buf, 8, None) == -1     # rows but no X
+    assert acc(None, 0, 8, 8, 0, buf, 8, None) == 0      # n == 0: nothing to add
+    assert fin(buf, 0, 8, 1.0, buf, 8, None) == -1
+    assert fin(buf, 8, 7, 1.0, buf, 8, None) == -1
+    assert fin(None, 8, 8, 1.0, buf, 8, None) == -1
