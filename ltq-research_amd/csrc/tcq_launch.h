@@ -36,6 +36,16 @@ struct GpuX {
     __device__ __forceinline__ int shfl_xor(int v, int m) const { return __shfl_xor(v, m, 64); }
     // instruction-scheduling barrier: nothing is moved across it (keeps loads issued ahead of the code they overlap)
     __device__ __forceinline__ void sched_fence() const { __builtin_amdgcn_sched_barrier(0); }
+    // 0, computed where it is used: offsets derived from it stay there instead of being hoisted out of loops
+    // (and held in registers across them)
+    __device__ __forceinline__ int opaque_zero() const
+    {
+        int z;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+        return z;
+    }
+    // v is computed at this point (not sunk past it), held in a vector register
+    __device__ __forceinline__ void pin(uint32_t& v) const { asm volatile("" : "+v"(v)); }
     // a value every lane holds equally, pinned to a scalar register
     __device__ __forceinline__ int uni(int v) const { return __builtin_amdgcn_readfirstlane(v); }
     // acquire at device scope: drops this CU's L1 lines, so global data rewritten since it was last read (by

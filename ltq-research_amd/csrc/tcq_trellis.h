@@ -611,8 +611,12 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
     uint32_t last_acc[NW];
 #pragma unroll
     for (int w = 0; w < NW; w++) last_acc[w] = 0;
-    auto chunk = [&](int c, auto FIRSTc) {
+    // AL (whole chunks, sub-blocks a multiple of 16 steps): a sub-block can only end where the phase's end step is
+    // a multiple of 16, so every other phase is compiled without the tile-end and merge tests (and without the
+    // register copies a runtime merge branch costs in every phase)
+    auto chunk = [&](int c, auto FIRSTc, auto ALc) {
         constexpr bool FIRST = decltype(FIRSTc)::value;
+        constexpr bool AL = decltype(ALc)::value;
 #pragma unroll
         for (int w = 0; w < NW; w++) acc[w] = 0;
         const float* tbn = s_tabs + ((c + 1) & 1) * TF;
@@ -621,12 +625,13 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
             constexpr int pi = decltype(PIc)::value;
             constexpr int PT = MM::PT(pi);
             const int ta = c * CK + 2 * pi;
-            if (ta >= T) {  // beyond the tile end: zero pushes keep every decision bit at its fixed position
+            if (!AL && ta >= T) {  // beyond the tile end: zero pushes keep every decision bit at its fixed position
 #pragma unroll
                 for (int i = 0; i < MM::PPH(PT); i++) LTQ_PUSH0(MM::OFF(pi) + i);
                 return;
             }
             real++;
+            if constexpr (AL) X_.sched_fence();  // one scheduling region per phase, as the runtime tests give the other build
             constexpr bool init = FIRST && pi == 0;
             static_for<0, NB>([&](auto Bc) {
                 constexpr int b = decltype(Bc)::value;
@@ -641,8 +646,14 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
 #pragma unroll
                     for (int j = 0; j < 4; j++) O[cc2][b][j] = Ob[cc2][j];
             });
+            if constexpr (AL) {  // the phase's decision bits are pushed now, not sunk to the chunk's word stores
+                constexpr int w0 = MM::OFF(pi) >> 5, w1 = (MM::OFF(pi + 1) - 1) >> 5;
+#pragma unroll
+                for (int w = w0; w <= w1; w++) X_.pin(acc[w]);
+            }
             const int tn = ta + 2;
-            if (tn >= T) return;  // last phase: outputs stay in registers for the argmin
+            constexpr bool MAYB = !AL || (2 * (pi + 1)) % 16 == 0;  // this phase may end the tile or a sub-block
+            if (MAYB && tn >= T) return;  // last phase: outputs stay in registers for the argmin
             // next phase's metrics: the tables were written before an earlier barrier, so the loads can fly
             // while this wave waits at the exchange barrier
             if constexpr (pi + 1 < NPC) {
@@ -671,7 +682,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                 }
             X_.lds_sync();
             if (pi == 0 && c + 1 < nchunk) tables(c + 1);  // next chunk's table (its buffer was last read in chunk c-1)
-            const bool at_sub = tn == next_merge;
+            const bool at_sub = MAYB && tn == next_merge;
             const int jm = merge_j;
             if (at_sub) {
                 next_merge += sub;
@@ -679,17 +690,22 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
             }
             if (!carry2 && G > 1 && at_sub) {
                 // gain merge: per state the lowest metric over the slots, lowest slot on ties (slots >= G read
-                // slot 0's value again, which never wins the strict compare)
+                // slot 0's value again, which never wins the strict compare). The slot bases are formed here, from
+                // an opaque zero, so they are not hoisted out of the chunk loop.
+                constexpr int GM = 16 / Q < 8 ? 16 / Q : 8;  // most gain slots this geometry serves
+                const float* xm[GM];
+                const int z0 = X_.opaque_zero();
+#pragma unroll
+                for (int gg = 0; gg < GM; gg++) xm[gg] = xmg + z0 + (gg < G ? gg * XF * S : 0);
 #pragma unroll
                 for (int b = 0; b < NB; b++)
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         const int s = GE::start((j << (RB - 2)) | b, q, lane);
                         const int so = ((j << (RB - 2)) | b) << (6 + QB);  // s - start(0, q, lane)
-                        constexpr int GM = 16 / Q < 8 ? 16 / Q : 8;  // most gain slots this geometry serves
                         float v[GM];
 #pragma unroll
-                        for (int gg = 0; gg < GM; gg++) v[gg] = gg < G ? xmg[gg * XF * S + so] : xmg[so];
+                        for (int gg = 0; gg < GM; gg++) v[gg] = xm[gg][so];
                         float bv = v[0];
                         int bg = 0;
 #pragma unroll
@@ -726,8 +742,13 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                 if (w < nwc) *dm.at(L0 + 64L * w) = acc[w];
         }
     };
-    chunk(0, std::true_type{});
-    for (int c = 1; c < nchunk; c++) chunk(c, std::false_type{});
+    if (T % CK == 0 && sub % 16 == 0) {
+        chunk(0, std::true_type{}, std::true_type{});
+        for (int c = 1; c < nchunk; c++) chunk(c, std::false_type{}, std::true_type{});
+    } else {
+        chunk(0, std::true_type{}, std::false_type{});
+        for (int c = 1; c < nchunk; c++) chunk(c, std::false_type{}, std::false_type{});
+    }
 
     // ---- argmin over (g, s), lowest index on ties (tcq_viterbi.cu:561-578) ---------------------------
     int bi_sel = 0;

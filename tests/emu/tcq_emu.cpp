@@ -63,6 +63,8 @@ struct CpuX {
     int load_coherent(const int* p) const { return *p; }
     void acquire() const {}
     void sched_fence() const {}
+    int opaque_zero() const { return 0; }
+    void pin(uint32_t&) const {}
     uint32_t readlane(uint32_t v, int l) const
     {
         const int w = tid_ >> 6;
