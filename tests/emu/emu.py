@@ -27,8 +27,9 @@ def build(asan: bool = False) -> Path:
 def lib(asan: bool = False):
     if asan not in _LIB:
         so = _DIR / ("libtcq_emu_asan.so" if asan else "libtcq_emu.so")
-        if not so.exists():
-            build(asan)
+        srcs = (_DIR / "tcq_emu.cpp", _DIR.parent.parent / "ltq-research_amd" / "csrc" / "tcq_trellis.h")
+        if not so.exists() or so.stat().st_mtime < max(f.stat().st_mtime for f in srcs):
+            build(asan)  # missing, or older than the kernel body it emulates
         L = ctypes.CDLL(str(so))
         L.tcq_viterbi_emu.restype = ctypes.c_int
         L.tcq_viterbi_emu.argtypes = [ctypes.c_void_p] * 15 + [ctypes.c_int] * 18 + [ctypes.c_void_p, ctypes.c_int]
