@@ -46,6 +46,29 @@ struct GpuX {
     }
     // v is computed at this point (not sunk past it), held in a vector register
     __device__ __forceinline__ void pin(uint32_t& v) const { asm volatile("" : "+v"(v)); }
+    // (value, index) minimum over the wavefront, lowest index on ties, left in lane 63: DPP row operations
+    // (quad swaps, half-row and row mirrors, then row broadcasts 15 and 31) instead of LDS permutes. The
+    // lexicographic minimum does not depend on the order of the combines.
+    template <int CTRL, int ROWS>
+    __device__ __forceinline__ static void dpp_min(float& bv, int& bi)
+    {
+        const int vb = __builtin_bit_cast(int, bv);
+        const float ov = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(vb, vb, CTRL, ROWS, 0xF, false));
+        const int oi = __builtin_amdgcn_update_dpp(bi, bi, CTRL, ROWS, 0xF, false);
+        if (ov < bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    __device__ __forceinline__ void wave_min(float& bv, int& bi) const
+    {
+        dpp_min<0xB1, 0xF>(bv, bi);   // quad_perm [1, 0, 3, 2]
+        dpp_min<0x4E, 0xF>(bv, bi);   // quad_perm [2, 3, 0, 1]
+        dpp_min<0x141, 0xF>(bv, bi);  // row_half_mirror
+        dpp_min<0x140, 0xF>(bv, bi);  // row_mirror: every lane of a row holds the row's minimum
+        dpp_min<0x142, 0xA>(bv, bi);  // row_bcast:15 into rows 1 and 3
+        dpp_min<0x143, 0xC>(bv, bi);  // row_bcast:31 into rows 2 and 3: lane 63 holds the wavefront's minimum
+    }
     // a value every lane holds equally, pinned to a scalar register
     __device__ __forceinline__ int uni(int v) const { return __builtin_amdgcn_readfirstlane(v); }
     // acquire at device scope: drops this CU's L1 lines, so global data rewritten since it was last read (by

@@ -768,16 +768,8 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                     bi = idx;
                 }
             }
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float ov = X_.shfl_xor(bv, off);
-            const int oi = X_.shfl_xor(bi, off);
-            if (ov < bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if (lane == 0) {
+        X_.wave_min(bv, bi);  // in lane 63
+        if (lane == 63) {
             s_rv[wv] = bv;
             s_ri[wv] = bi;
         }
@@ -787,17 +779,9 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
             const int nw = nthr / 64;
             bv = lane < nw ? s_rv[lane] : kSent;
             bi = lane < nw ? s_ri[lane] : 0x7fffffff;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float ov = X_.shfl_xor(bv, off);
-                const int oi = X_.shfl_xor(bi, off);
-                if (ov < bv || (ov == bv && oi < bi)) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
+            X_.wave_min(bv, bi);
         }
-        bi_sel = (int)X_.readlane((uint32_t)bi, 0);
+        bi_sel = (int)X_.readlane((uint32_t)bi, 63);
         if (bi_sel == 0x7fffffff) bi_sel = 0;  // no candidate at or below the sentinel: the reference reads out of range
     }
     const int bi_all = X_.uni(bi_sel);  // uniform: scalar registers

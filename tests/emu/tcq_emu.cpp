@@ -65,6 +65,18 @@ struct CpuX {
     void sched_fence() const {}
     int opaque_zero() const { return 0; }
     void pin(uint32_t&) const {}
+    // (value, index) minimum over the wavefront, lowest index on ties, in every lane (the GPU leaves it in lane 63)
+    void wave_min(float& bv, int& bi) const
+    {
+        for (int off = 1; off < 64; off <<= 1) {
+            const float ov = shfl_xor(bv, off);
+            const int oi = shfl_xor(bi, off);
+            if (ov < bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+    }
     uint32_t readlane(uint32_t v, int l) const
     {
         const int w = tid_ >> 6;
