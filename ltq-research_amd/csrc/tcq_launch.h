@@ -32,8 +32,6 @@ struct GpuX {
         return __builtin_amdgcn_alignbit(acc, __builtin_bit_cast(uint32_t, d), 31);
     }
     __device__ __forceinline__ float fmin(float x, float y) const { return __builtin_fminf(x, y); }
-    __device__ __forceinline__ float shfl_xor(float v, int m) const { return __shfl_xor(v, m, 64); }
-    __device__ __forceinline__ int shfl_xor(int v, int m) const { return __shfl_xor(v, m, 64); }
     // instruction-scheduling barrier: nothing is moved across it (keeps loads issued ahead of the code they overlap)
     __device__ __forceinline__ void sched_fence() const { __builtin_amdgcn_sched_barrier(0); }
     // 0, computed where it is used: offsets derived from it stay there instead of being hoisted out of loops

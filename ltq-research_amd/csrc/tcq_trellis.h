@@ -406,10 +406,11 @@ struct DecMap {
 // ------------------------------------------------------------------------------------------------
 // The per-tile kernel body.
 // X provides: tid(), wave() (tid / 64, uniform), tile(), nthreads(), smem(), sync() (full barrier incl. global
-// memory), lds_sync() (barrier for LDS only), push_sign(acc, d), fmin(x, y), shfl_xor(v, mask) (within a
-// wavefront), readlane(v, l) (lane l's value, l uniform), uni(v) (a uniform value in a scalar register),
-// load_coherent(p) (a global int written by this workgroup before a sync()), acquire() (device-scope acquire:
-// invalidates this CU's L1), load16(global src, LDS wave base) (asynchronous 16-byte
+// memory), lds_sync() (barrier for LDS only), push_sign(acc, d), fmin(x, y), wave_min(v, i) (the wavefront's
+// (value, index) minimum, lowest index on ties, in lane 63), readlane(v, l) (lane l's value, l uniform), uni(v)
+// (a uniform value in a scalar register), pin(v) (v computed at this point), sched_fence() (no instruction
+// moved across), load_coherent(p) (a global int written by this workgroup before a sync()), acquire()
+// (device-scope acquire: invalidates this CU's L1), load16(global src, LDS wave base) (asynchronous 16-byte
 // global -> LDS copy landing at base + 16 * lane), wait_loads(n) (at most n such copies of this wave still
 // outstanding, n <= 63).
 // ------------------------------------------------------------------------------------------------
