@@ -733,10 +733,17 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
         const int rbits = TWO ? (real / 2) * (MM::PPH(0) + MM::PPH(1)) + (real & 1) * MM::PPH(0) : real * MM::PPH(0);
         const int nwc = real == NPC ? NW : (rbits + 31) / 32;
         // word-major: word w of every lane of (slot g, wave q) is 64 consecutive u32 (coalesced stores)
-        const long L0 = (long)c * chunk_words + (long)(g * Q + q) * nwc * 64 + lane;
+        const long Lb = (long)c * chunk_words + (long)(g * Q + q) * nwc * 64;  // uniform: the wave's first word
+        const long L0 = Lb + lane;
         if (fast && c == nchunk - 1) {
 #pragma unroll
             for (int w = 0; w < NW; w++) last_acc[w] = acc[w];
+        } else if (Lb + 64L * nwc <= dm.cap_bp || Lb >= dm.cap_bp) {
+            // the wave's words lie in one buffer: a scalar base, the lane offset and immediate word offsets
+            uint32_t* const wb = Lb < dm.cap_bp ? dm.bp + Lb : dm.pb + (Lb - dm.cap_bp);
+#pragma unroll
+            for (int w = 0; w < NW; w++)
+                if (w < nwc) wb[lane + 64 * w] = acc[w];
         } else {
 #pragma unroll
             for (int w = 0; w < NW; w++)
