@@ -241,9 +241,9 @@ LTQ_DEV float level_err(float xt, float gain, const float* tb, int u0, int Ut, i
 // high state bit wins only when strictly smaller (p0 on ties), as in the reference.
 // ma[jj][p]: metric of intermediate jj (step a), mb[j][p]: metric of output j (step b), p = parity class.
 // ------------------------------------------------------------------------------------------------
-template <int MD, int PT, int P0, bool init, class X>
+template <int MD, int PT, int P0, bool init, class X, class HA, class HB>
 LTQ_DEV void run_block(const bool (&ok)[4], const float (&I)[2][4], const float (&ma)[4][2],
-                       const float (&mb)[4][2], float (&O)[2][4], uint32_t* acc, X& X_)
+                       const float (&mb)[4][2], float (&O)[2][4], uint32_t* acc, X& X_, HA&& ha, HB&& hb)
 {
     constexpr bool EQ = MD == 3;
     if constexpr (MD == 0) {
@@ -261,6 +261,7 @@ LTQ_DEV void run_block(const bool (&ok)[4], const float (&I)[2][4], const float 
                 v[j0] = m + ma[j0][0];
                 v[j1] = m + ma[j1][0];
             }
+            ha(e);
         }
 #pragma unroll
         for (int f = 0; f < 2; f++) {
@@ -269,6 +270,7 @@ LTQ_DEV void run_block(const bool (&ok)[4], const float (&I)[2][4], const float 
             LTQ_CSP(P0 + 2 + f, v[j1], v[j0], m);
             O[0][j0] = m + mb[j0][0];
             O[0][j1] = m + mb[j1][0];
+            hb(f);
         }
     } else if constexpr (PT == 0) {
         // D2 pair, or phase A of a D4 / EQ group: intermediates per low bit b of the first sample
@@ -292,6 +294,7 @@ LTQ_DEV void run_block(const bool (&ok)[4], const float (&I)[2][4], const float 
                 I0[j1] = m + ma[j1][0];
                 I1[j1] = m + ma[j1][1];
             }
+            ha(e);
         }
         constexpr int PB = MD == 1 ? 4 : MD == 2 ? 6 : 2;
 #pragma unroll
@@ -326,6 +329,7 @@ LTQ_DEV void run_block(const bool (&ok)[4], const float (&I)[2][4], const float 
                     O[1][r] = m1 + mb[r][1];
                 }
             }
+            hb(f);
         }
     } else if constexpr (!EQ) {
         // D4 phase B: J[c][b] = min over predecessors of C_c + E(b); output = best (c, b) in order 00,01,10,11
@@ -344,6 +348,7 @@ LTQ_DEV void run_block(const bool (&ok)[4], const float (&I)[2][4], const float 
                 J[2][jj] = mc1 + ma[jj][0];
                 J[3][jj] = mc1 + ma[jj][1];
             }
+            ha(e);
         }
 #pragma unroll
         for (int f = 0; f < 2; f++) {
@@ -360,6 +365,7 @@ LTQ_DEV void run_block(const bool (&ok)[4], const float (&I)[2][4], const float 
                 LTQ_CSP(PF + 4 + 3 * qq + 2, mm[3] + mb[r][0], v, v);
                 O[0][r] = v;
             }
+            hb(f);
         }
     } else {
         // EQ phase B: classes keep b = c; output = best class (ties: c = 0)
@@ -376,6 +382,7 @@ LTQ_DEV void run_block(const bool (&ok)[4], const float (&I)[2][4], const float 
                 Jc[0][jj] = mc0 + ma[jj][0];
                 Jc[1][jj] = mc1 + ma[jj][1];
             }
+            ha(e);
         }
 #pragma unroll
         for (int f = 0; f < 2; f++) {
@@ -390,6 +397,7 @@ LTQ_DEV void run_block(const bool (&ok)[4], const float (&I)[2][4], const float 
                 LTQ_CSP(PF + 2 + qq, m1 + mb[r][1], m0 + mb[r][0], o);
                 O[0][r] = o;
             }
+            hb(f);
         }
     }
 }
@@ -634,6 +642,13 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
             real++;
             if constexpr (AL) X_.sched_fence();  // one scheduling region per phase, as the runtime tests give the other build
             constexpr bool init = FIRST && pi == 0;
+            // The next phase's metrics are loaded while this phase computes, each pair of slots as soon as its
+            // step has consumed it (the LDS reads then stream beside the compare-selects instead of queueing
+            // with the exchange stores at the barrier). The last phase of a chunk reads the next chunk's table
+            // (written in this chunk's phase 0, visible since phase 1's barrier); loads past the tile's last
+            // phase stay inside the table and are unused.
+            constexpr int PN = (pi + 1) % NPC;
+            if constexpr (pi + 1 == NPC) point_metrics(tbn);
             static_for<0, NB>([&](auto Bc) {
                 constexpr int b = decltype(Bc)::value;
                 float Ib[2][4], Ob[2][4];
@@ -641,7 +656,27 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                 for (int cc2 = 0; cc2 < 2; cc2++)
 #pragma unroll
                     for (int j = 0; j < 4; j++) Ib[cc2][j] = I[cc2][b][j];
-                run_block<MD, PT, MM::OFF(pi) + b * MM::PBLK(PT), init>(ok[b], Ib, ma[b], mb[b], Ob, acc, X_);
+                // (scheduling fences keep the compiler from sinking the loads to the end of the phase)
+                auto ha = [&](int e) {  // step a used slots e, 2 + e of ma
+                    X_.sched_fence();
+#pragma unroll
+                    for (int p = 0; p < NP; p++) {
+                        ma[b][e][p] = pma[b][e][(2 * PN) * NL * NP + p];
+                        ma[b][2 + e][p] = pma[b][2 + e][(2 * PN) * NL * NP + p];
+                    }
+                    X_.sched_fence();
+                };
+                auto hb = [&](int f) {  // step b used slots 2 f, 2 f + 1 of mb
+                    X_.sched_fence();
+#pragma unroll
+                    for (int p = 0; p < NP; p++) {
+                        mb[b][2 * f][p] = pmb[b][2 * f][(2 * PN + 1) * NL * NP + p];
+                        mb[b][2 * f + 1][p] = pmb[b][2 * f + 1][(2 * PN + 1) * NL * NP + p];
+                    }
+                    X_.sched_fence();
+                };
+                run_block<MD, PT, MM::OFF(pi) + b * MM::PBLK(PT), init>(ok[b], Ib, ma[b], mb[b], Ob, acc, X_, ha,
+                                                                        hb);
 #pragma unroll
                 for (int cc2 = 0; cc2 < 2; cc2++)
 #pragma unroll
@@ -655,14 +690,6 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
             const int tn = ta + 2;
             constexpr bool MAYB = !AL || (2 * (pi + 1)) % 16 == 0;  // this phase may end the tile or a sub-block
             if (MAYB && tn >= T) return;  // last phase: outputs stay in registers for the argmin
-            // next phase's metrics: the tables were written before an earlier barrier, so the loads can fly
-            // while this wave waits at the exchange barrier
-            if constexpr (pi + 1 < NPC) {
-                load_metrics(std::integral_constant<int, pi + 1>{});
-            } else {
-                point_metrics(tbn);
-                load_metrics(std::integral_constant<int, 0>{});
-            }
             // ---- exchange into the next phase's start layout (+ gain merge at a sub-block boundary) ----
             constexpr bool carry2 = TWO && PT == 0;  // phase A -> B carries two class planes
             const int xo = (pi & 1) ? xs_1 : 0;
@@ -682,7 +709,6 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                     *(F4*)(xst + cp * S + (b << (8 + QB))) = v4;
                 }
             X_.lds_sync();
-            if (pi == 0 && c + 1 < nchunk) tables(c + 1);  // next chunk's table (its buffer was last read in chunk c-1)
             const bool at_sub = MAYB && tn == next_merge;
             const int jm = merge_j;
             if (at_sub) {
@@ -727,6 +753,8 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                         for (int j = 0; j < 4; j++)  // slot j of block b is register (j << (RB - 2)) | b
                             I[cp][b][j] = xld[cp * S + (((j << (RB - 2)) | b) << (6 + QB))];
             }
+            // next chunk's table (its buffer was last read in chunk c-1), built while the exchange loads fly
+            if (pi == 0 && c + 1 < nchunk) tables(c + 1);
         });
         // ---- store this chunk's decision words (left-aligned), only the words holding real bits -------
         if (MM::LAST < 32) acc[NW - 1] <<= (32 - MM::LAST) & 31;
