@@ -724,26 +724,40 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                 const int z0 = X_.opaque_zero();
 #pragma unroll
                 for (int gg = 0; gg < GM; gg++) xm[gg] = xmg + z0 + (gg < G ? gg * XF * S : 0);
+                if (g == 0) {  // slot 0's wavefronts also record the merge choice for the traceback
 #pragma unroll
-                for (int b = 0; b < NB; b++)
+                    for (int b = 0; b < NB; b++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const int s = GE::start((j << (RB - 2)) | b, q, lane);
-                        const int so = ((j << (RB - 2)) | b) << (6 + QB);  // s - start(0, q, lane)
-                        float v[GM];
+                        for (int j = 0; j < 4; j++) {
+                            const int s = GE::start((j << (RB - 2)) | b, q, lane);
+                            const int so = ((j << (RB - 2)) | b) << (6 + QB);  // s - start(0, q, lane)
+                            float v[GM];
 #pragma unroll
-                        for (int gg = 0; gg < GM; gg++) v[gg] = xm[gg][so];
-                        float bv = v[0];
-                        int bg = 0;
+                            for (int gg = 0; gg < GM; gg++) v[gg] = xm[gg][so];
+                            float bv = v[0];
+                            int bg = 0;
 #pragma unroll
-                        for (int gg = 1; gg < GM; gg++)
-                            if (v[gg] < bv) {
-                                bv = v[gg];
-                                bg = gg;
-                            }
-                        I[0][b][j] = bv;
-                        if (g == 0) s_gsel[jm * S + s] = (uint8_t)bg;
-                    }
+                            for (int gg = 1; gg < GM; gg++)
+                                if (v[gg] < bv) {
+                                    bv = v[gg];
+                                    bg = gg;
+                                }
+                            I[0][b][j] = bv;
+                            s_gsel[jm * S + s] = (uint8_t)bg;
+                        }
+                } else {  // the merged metric alone: the minimum over the slots (the value the lowest-slot rule
+                          // selects, as no metric is NaN or -0), a third of the VALU on three of four SIMD slots
+#pragma unroll
+                    for (int b = 0; b < NB; b++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int so = ((j << (RB - 2)) | b) << (6 + QB);
+                            float bv = xm[0][so];
+#pragma unroll
+                            for (int gg = 1; gg < GM; gg++) bv = X_.fmin(bv, xm[gg][so]);
+                            I[0][b][j] = bv;
+                        }
+                }
             } else {
 #pragma unroll
                 for (int cp = 0; cp < (carry2 ? 2 : 1); cp++)
