@@ -802,8 +802,23 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
 
     // ---- argmin over (g, s), lowest index on ties (tcq_viterbi.cu:561-578) ---------------------------
     int bi_sel = 0;
-    {
-        const int s_end = a.tail ? s0 : -1;
+    const int s_end = a.tail ? s0 : -1;
+    if (s_end >= 0 && s_end < S) {
+        // Closing pass: every (slot, state) but state s_end of each slot enters the argmin at the sentinel, so the
+        // lexicographic minimum is the one over the G candidates (value of s_end in slot g, index g S + s_end)
+        // and the lowest-index sentinel entry (kSent, s_end ? 0 : 1). The lane holding s_end in each slot stores
+        // its value; one reduction over G + 1 lanes follows the barrier (no per-wavefront reduction before it).
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (GE::end(b, j, q, lane) == s_end) s_rv[g] = O[0][b][j];
+        X_.sync();  // full barrier: also completes every wave's decision-word stores before the traceback
+        float bv = lane < G ? s_rv[lane] : kSent;
+        int bi = lane < G ? lane * S + s_end : lane == 63 ? (s_end != 0 ? 0 : 1) : 0x7fffffff;
+        X_.wave_min(bv, bi);
+        bi_sel = (int)X_.readlane((uint32_t)bi, 63);
+    } else {
         float bv = kSent;
         int bi = 0x7fffffff;
 #pragma unroll
