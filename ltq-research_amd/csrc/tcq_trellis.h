@@ -814,10 +814,12 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
             for (int j = 0; j < 4; j++)
                 if (GE::end(b, j, q, lane) == s_end) s_rv[g] = O[0][b][j];
         X_.sync();  // full barrier: also completes every wave's decision-word stores before the traceback
-        float bv = lane < G ? s_rv[lane] : kSent;
-        int bi = lane < G ? lane * S + s_end : lane == 63 ? (s_end != 0 ? 0 : 1) : 0x7fffffff;
-        X_.wave_min(bv, bi);
-        bi_sel = (int)X_.readlane((uint32_t)bi, 63);
+        if (wv == 0) {  // only the walking wavefront uses the result (the others keep an in-range 0)
+            float bv = lane < G ? s_rv[lane] : kSent;
+            int bi = lane < G ? lane * S + s_end : lane == 63 ? (s_end != 0 ? 0 : 1) : 0x7fffffff;
+            X_.wave_min(bv, bi);
+            bi_sel = (int)X_.readlane((uint32_t)bi, 63);
+        }
     } else {
         float bv = kSent;
         int bi = 0x7fffffff;
@@ -839,15 +841,16 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
             s_ri[wv] = bi;
         }
         X_.sync();  // full barrier: also completes every wave's decision-word stores before the traceback
-        // every wavefront reduces the per-wavefront results across its lanes (no second barrier)
-        {
+        // the walking wavefront reduces the per-wavefront results across its lanes (no second barrier); the
+        // others keep an in-range 0
+        if (wv == 0) {
             const int nw = nthr / 64;
             bv = lane < nw ? s_rv[lane] : kSent;
             bi = lane < nw ? s_ri[lane] : 0x7fffffff;
             X_.wave_min(bv, bi);
+            bi_sel = (int)X_.readlane((uint32_t)bi, 63);
+            if (bi_sel == 0x7fffffff) bi_sel = 0;  // no candidate at or below the sentinel: the reference reads out of range
         }
-        bi_sel = (int)X_.readlane((uint32_t)bi, 63);
-        if (bi_sel == 0x7fffffff) bi_sel = 0;  // no candidate at or below the sentinel: the reference reads out of range
     }
     const int bi_all = X_.uni(bi_sel);  // uniform: scalar registers
 
