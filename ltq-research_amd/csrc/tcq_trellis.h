@@ -521,6 +521,39 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
     const int TF = SM.tab_floats;
     auto tables = [&](int cc) {
         float* tb = s_tabs + (cc & 1) * TF;
+        // one entry per thread, the slot's own gain, two levels per parity class at most (the D4 formats with
+        // 8-subset labels, as in the matrix path): straight-line, the level loop of level_err unrolled
+        if constexpr (MD != 0 && CK * NL * NP == 64 * Q) {
+            if (!cand && (U == 2 || U == 4)) {
+                const int e = tid;
+                const int p = e & 1, lb = (e / NP) % NL, k = (e / (NP * NL)) % CK, gg = e / (NP * NL * CK);
+                const int t = cc * CK + k;
+                float E = 0.f;
+                if (t < T) {
+                    const float gain = s_gain[gg];
+                    const float xt = s_x[t];
+                    const float* tl = s_tab + lb * U + p;  // levels p and p + 2 of label lb
+                    const float l0 = tl[0], l1 = tl[2];   // tl[2] lies inside s_tab (4 kMaxU floats) also for U = 2
+                    float be = kSent;
+                    {
+                        const float v = gain * l0;
+                        const float d = xt - v;
+                        const float dd = d * d;
+                        be = dd < be ? dd : be;
+                    }
+                    if (U == 4) {
+                        const float v = gain * l1;
+                        const float d = xt - v;
+                        const float dd = d * d;
+                        be = dd < be ? dd : be;
+                    }
+                    E = be * s_w[t];
+                    E = E + 0.0f;
+                }
+                tb[e] = E;
+                return;
+            }
+        }
         for (int e = tid; e < TF; e += nthr) {
             const int p = NP == 2 ? (e & 1) : 0;
             const int lb = (e / NP) % NL, k = (e / (NP * NL)) % CK, gg = e / (NP * NL * CK);
