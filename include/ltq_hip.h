@@ -95,11 +95,14 @@ int ltq_pack_rings(const int16_t* idx, long ld_idx, const uint8_t* gi, long ld_g
 /* Row scale of a rotated weight matrix w [M, K] (K % 256 == 0, row stride ldw, 16-byte aligned):
  * rms of every 256-column block (clamped at 1e-10, times scale), d_row[M] = fp16-rounded geometric mean of
  * the row's block rms (clamped at 1e-8), e[M, K/256] (int8, row stride lde) = clamp(round(log2(rms / d_row)
- * / e_step), -2^(e_bits-1), 2^(e_bits-1) - 1) and d[M, K/256] (row stride ldd) = max(d_row 2^(e_step e), 1e-8).
- * Replaces the torch code src/liqk_v2.py:938-946 (and the clamp of :959); agrees with it to fp32 rounding of
- * the reductions and transcendental functions. */
-int ltq_row_scale(const float* w, long M, long K, long ldw, float scale, float e_step, int e_bits, float* d_row,
-                  int8_t* e, long lde, float* d, long ldd, void* stream);
+ * / e_step), -2^(e_bits-1), 2^(e_bits-1) - 1) and d[M, K/256] (row stride ldd) = max(d_row * exp2_tab[e +
+ * 2^(e_bits-1)], 1e-8). exp2_tab: device array of 2^e_bits floats, entry k = 2^(e_step (k - 2^(e_bits-1)))
+ * rounded once to fp32 on the host (the table the .ltq decoder uses). Replaces the torch code
+ * src/liqk_v2.py:938-946 (and the clamp of :959); its results are defined to the bit: fixed-order block sums
+ * (per 4-element group left to right, then a lane butterfly over offsets 32..1), correctly rounded fp32 sqrt,
+ * log / mean / exp and log2 in float64, round half to even. */
+int ltq_row_scale(const float* w, long M, long K, long ldw, float scale, float e_step, int e_bits,
+                  const float* exp2_tab, float* d_row, int8_t* e, long lde, float* d, long ldd, void* stream);
 
 /* First Viterbi input of a 256-column block: x[T, 256] tiles (t = 16 r + c) = wk[:, 0:16] * (1 / d[row])
  * (src/liqk_v2.py:955-958, the `w_sub_orig * inv_d` of sub-block 0). M % 16 == 0; d has row stride ldd. */

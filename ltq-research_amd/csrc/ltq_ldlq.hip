@@ -1,8 +1,17 @@
 // Row scale fitting and the LDLQ sub-block error feedback of the TCQ matrix quantizer, gfx950.
 //
 // ltq_row_scale (src/liqk_v2.py:938-946): per row, the rms of every 256-column block (clamped at 1e-10, times
-// the format scale), d_row = fp16(exp(mean over blocks of log rms)) clamped at 1e-8, the 5-bit block exponent
+// the format scale), d_row = fp16(exp(mean over blocks of log rms)) clamped at 1e-8, the block exponent
 // e = clamp(round(log2(rms / d_row) / e_step), -2^(bits-1), 2^(bits-1) - 1) and d = d_row * 2^(e_step e).
+// The result is defined to the bit, so that a CPU restatement reproduces it exactly:
+//   - block sum of squares: lane l holds ((x[4l]^2 + x[4l+1]^2) + x[4l+2]^2) + x[4l+3]^2, then a butterfly over
+//     lane offsets 32, 16, 8, 4, 2, 1 (s_l + s_(l^o): every lane ends with the same bits); rms = sqrt(s / 256),
+//     all fp32, correctly rounded;
+//   - log, mean and exp in float64 (sequential sum over the blocks), rounded to fp32 and then to fp16; the
+//     exponent from the fp32 ratio rms / d_row as round-half-even of log2(ratio) / e_step in float64: float64
+//     keeps every value far from the fp16 / half-step rounding boundaries the fp32 functions can straddle;
+//   - 2^(e_step e) is read from a host-computed table (float64, rounded once to fp32), the same table the PACK
+//     tail, the .ltq decoder and the CPU oracle use.
 // One wavefront per row. Roofline: HBM, 4 bytes read per weight.
 //
 // ltq_ldlq_sub (src/liqk_v2.py:957-967): after the Viterbi of sub-block ib of a 256-column block, for the 16
@@ -25,7 +34,8 @@
 namespace {
 
 __global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict__ w, long M, int nblk, long ldw,
-                                                        float scale, float e_step, int e_max, float* __restrict__ d_row,
+                                                        float scale, double e_step, int e_max,
+                                                        const float* __restrict__ exp2_tab, float* __restrict__ d_row,
                                                         int8_t* __restrict__ e_out, long lde, float* __restrict__ d_out,
                                                         long ldd)
 {
@@ -35,7 +45,7 @@ __global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict_
     if (row >= M) return;
     float* rms = s_rms + wv * nblk;
     const float* wr = w + row * ldw;
-    float lsum = 0.f;
+    double lsum = 0.0;
     for (int b = 0; b < nblk; b++) {
         const float4 v = *(const float4*)(wr + b * 256 + 4 * lane);
         float s = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
@@ -43,18 +53,20 @@ __global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict_
         for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
         const float r = fmaxf(sqrtf(s / 256.f), 1e-10f) * scale;
         if (lane == 0) rms[b] = r;
-        lsum += logf(r);  // every lane holds the same r
+        lsum += log((double)r);  // every lane holds the same r
     }
-    const float d = fmaxf(__half2float(__float2half(expf(lsum / (float)nblk))), 1e-8f);
+    const float d = fmaxf(__half2float(__float2half((float)exp(lsum / (double)nblk))), 1e-8f);
     if (lane == 0) d_row[row] = d;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     for (int b = lane; b < nblk; b += 64) {
-        float e = rintf(log2f(rms[b] / d) / e_step);
-        e = fminf(fmaxf(e, (float)-e_max), (float)(e_max - 1));
-        e_out[row * lde + b] = (int8_t)e;
-        d_out[row * ldd + b] = fmaxf(d * exp2f(e_step * e), 1e-8f);
+        const float ratio = rms[b] / d;
+        double e = rint(log2((double)ratio) / e_step);
+        e = fmin(fmax(e, (double)-e_max), (double)(e_max - 1));
+        const int ei = (int)e;
+        e_out[row * lde + b] = (int8_t)ei;
+        d_out[row * ldd + b] = fmaxf(d * exp2_tab[ei + e_max], 1e-8f);
     }
 }
 
@@ -121,16 +133,17 @@ __global__ __launch_bounds__(256) void ldlq_prep_kernel(const float* __restrict_
 }  // namespace
 
 extern "C" int ltq_row_scale(const float* w, long M, long K, long ldw, float scale, float e_step, int e_bits,
-                             float* d_row, int8_t* e, long lde, float* d, long ldd, void* stream)
+                             const float* exp2_tab, float* d_row, int8_t* e, long lde, float* d, long ldd, void* stream)
 {
     if (M < 0 || K < 0 || K % 256 || ldw < K || (ldw & 3) || e_bits < 1 || e_bits > 8 || !(e_step > 0.f) || !(scale > 0.f))
         return -1;
     const int nblk = (int)(K / 256);
     if (M == 0 || nblk == 0) return 0;
-    if (!w || !d_row || !e || !d || lde < nblk || ldd < nblk || ((uintptr_t)w & 15) || nblk > 4096) return -1;
+    if (!w || !exp2_tab || !d_row || !e || !d || lde < nblk || ldd < nblk || ((uintptr_t)w & 15) || nblk > 4096)
+        return -1;
     const long grid = (M + 3) / 4;
     hipLaunchKernelGGL(row_scale_kernel, dim3((unsigned)grid), dim3(256), 4 * 4 * nblk, (hipStream_t)stream, w, M, nblk,
-                       ldw, scale, e_step, 1 << (e_bits - 1), d_row, e, lde, d, ldd);
+                       ldw, scale, (double)e_step, 1 << (e_bits - 1), exp2_tab, d_row, e, lde, d, ldd);
     return (int)hipGetLastError();
 }
 

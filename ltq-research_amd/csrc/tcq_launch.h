@@ -120,6 +120,20 @@ __global__ __launch_bounds__(1024, WMIN) void tcq_viterbi_kernel(TcqArgs a, int 
 int device_lds_max();
 int device_cu_count();
 
+// hipFuncSetAttribute(f, max dynamic LDS, bytes) once per (kernel, device): done[] is the caller's per-kernel
+// flag array; a failed call is returned and retried at the next launch
+template <class K>
+int set_max_lds_once(K* kernel, int bytes, bool (&done)[64])
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return -1;
+    if (dev >= 0 && dev < 64 && done[dev]) return 0;
+    const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return (int)e;
+    if (dev >= 0 && dev < 64) done[dev] = true;
+    return 0;
+}
+
 // Both tail-biting passes of every tile in one launch.
 template <int NU, int RB, int MD, int NL>
 __global__ __launch_bounds__(1024) void tcq_viterbi_tb_kernel(TcqArgs a1, TcqArgs a2, int lds_max)
@@ -138,12 +152,8 @@ int launch(const TcqArgs& a, hipStream_t stream)
         const int half = lds_max / 2;
         const Smem H = smem_layout<NU, RB, MD, NL>(a.T, a.G, a.Gfull, a.sub, half);
         if (cus > 0 && a.N >= 2 * cus && H.total <= half) {
-            static bool attr2 = false;
-            if (!attr2) {
-                (void)hipFuncSetAttribute((const void*)tcq_viterbi_kernel<NU, RB, MD, NL, 8>,
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, half);
-                attr2 = true;
-            }
+            static bool attr2[64] = {};
+            if (const int e = set_max_lds_once(tcq_viterbi_kernel<NU, RB, MD, NL, 8>, half, attr2)) return e;
             const int threads = 64 * a.G * Geo<NU, RB>::Q;
             hipLaunchKernelGGL((tcq_viterbi_kernel<NU, RB, MD, NL, 8>), dim3(a.N), dim3(threads), H.total, stream, a,
                                half);
@@ -152,12 +162,8 @@ int launch(const TcqArgs& a, hipStream_t stream)
     }
     const Smem L = smem_layout<NU, RB, MD, NL>(a.T, a.G, a.Gfull, a.sub, lds_max);
     if (L.total > lds_max) return -1;
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute((const void*)tcq_viterbi_kernel<NU, RB, MD, NL>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
-        attr = true;
-    }
+    static bool attr[64] = {};
+    if (const int e = set_max_lds_once(tcq_viterbi_kernel<NU, RB, MD, NL>, lds_max, attr)) return e;
     const int threads = 64 * a.G * Geo<NU, RB>::Q;
     hipLaunchKernelGGL((tcq_viterbi_kernel<NU, RB, MD, NL>), dim3(a.N), dim3(threads), L.total, stream, a, lds_max);
     return 0;
@@ -172,12 +178,8 @@ int launch_tb(const TcqArgs& a1, const TcqArgs& a2, hipStream_t stream)
     const Smem L2 = smem_layout<NU, RB, MD, NL>(a2.T, a2.G, a2.Gfull, a2.sub, lds_max);
     const int total = L1.total > L2.total ? L1.total : L2.total;
     if (total > lds_max) return -1;
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute((const void*)tcq_viterbi_tb_kernel<NU, RB, MD, NL>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds_max);
-        attr = true;
-    }
+    static bool attr[64] = {};
+    if (const int e = set_max_lds_once(tcq_viterbi_tb_kernel<NU, RB, MD, NL>, lds_max, attr)) return e;
     const int threads = 64 * a2.G * Geo<NU, RB>::Q;
     hipLaunchKernelGGL((tcq_viterbi_tb_kernel<NU, RB, MD, NL>), dim3(a2.N), dim3(threads), total, stream, a1, a2,
                        lds_max);

@@ -26,28 +26,29 @@ LTQ_EXT_MD(0) LTQ_EXT_MD(1) LTQ_EXT_MD(2) LTQ_EXT_MD(3)
 #undef LTQ_EXT_MD
 #undef LTQ_EXT
 
+// per-device attributes of the current device, cached per device ordinal (a process may drive several GPUs)
+constexpr int kMaxDevices = 64;
+
+static int device_attr(hipDeviceAttribute_t attr, int (&cache)[kMaxDevices])
+{
+    int dev = 0, x = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return -1;
+    if (dev < kMaxDevices && cache[dev] > 0) return cache[dev];
+    if (hipDeviceGetAttribute(&x, attr, dev) != hipSuccess) return -1;
+    if (dev < kMaxDevices) cache[dev] = x;
+    return x;
+}
+
 int device_lds_max()
 {
-    static int v = -1;
-    if (v < 0) {
-        int dev = 0, x = 0;
-        if (hipGetDevice(&dev) != hipSuccess) return -1;
-        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) return -1;
-        v = x;
-    }
-    return v;
+    static int cache[kMaxDevices] = {};
+    return device_attr(hipDeviceAttributeMaxSharedMemoryPerBlock, cache);
 }
 
 int device_cu_count()
 {
-    static int v = -1;
-    if (v < 0) {
-        int dev = 0, x = 0;
-        if (hipGetDevice(&dev) != hipSuccess) return -1;
-        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
-        v = x;
-    }
-    return v;
+    static int cache[kMaxDevices] = {};
+    return device_attr(hipDeviceAttributeMultiprocessorCount, cache);
 }
 
 struct GpuLaunch {

@@ -34,7 +34,7 @@ SIGNATURES = {
     # src/liqk_v2.py:207-231 (_CovAccumulator.add / get)
     "ltq_cov_accumulate": (ci, [vp, cl, ci, cl, ci, vp, cl, vp]),
     "ltq_cov_finalize": (ci, [vp, ci, cl, cd, vp, cl, vp]),
-    "ltq_row_scale": (ci, [vp, cl, cl, cl, cf, cf, ci, vp, vp, cl, vp, cl, vp]),
+    "ltq_row_scale": (ci, [vp, cl, cl, cl, cf, cf, ci, vp, vp, vp, cl, vp, cl, vp]),
     "ltq_ldlq_prep": (ci, [vp, cl, vp, cl, vp, cl, vp]),
     "ltq_ldlq_sub": (ci, [vp, cl, vp, vp, cl, vp, cl, vp, cl, ci, vp, cl, vp, cl, vp, vp, cl, vp, cl, vp]),
 }

@@ -2,7 +2,7 @@
 
 Mirrors src/liqk_v2.py:779-840 (TCQ_CONFIG construction), src/ltq_format.py:16-66 (NU, TILE, MASK_M,
 LtqFormat, load_formats) and src/equal_bpw.py:42-75 (SETS menus). The trained tables themselves are data,
-extracted unchanged into data/tcq_tables.json (see data/make_tables.py).
+extracted unchanged into data/tcq_tables.json by tests/golden/make_tables.py.
 """
 from __future__ import annotations
 
@@ -62,6 +62,18 @@ SETS = {
 }
 
 FRAC_RATE = {0: 0.0, 1: 0.5, 2: 0.25, 3: 0.75}
+
+# row-scale block exponent (src/liqk_v2.py:943-946): d = d_row * 2^(E_STEP * e), e in [-2^(E_BITS-1), 2^(E_BITS-1))
+E_STEP, E_BITS = 0.25, 5
+
+
+def exp2_table(e_step: float = E_STEP, e_bits: int = E_BITS) -> np.ndarray:
+    """float32 [2^e_bits]: entry k = 2^(e_step * (k - 2^(e_bits-1))), evaluated in float64 and rounded once to
+    float32. The one table of block-exponent factors: the quantizer's row scale, the PACK tail, the .ltq decoder
+    (assemble) and the CPU oracle all read it, so the scale d of a block is the same bits everywhere. For the
+    .ltq exponent (e_step 0.25, 5 bits) it equals torch's float32 exp2(0.25 * e) entry for entry."""
+    half = 1 << (e_bits - 1)
+    return np.array([2.0 ** (e_step * (k - half)) for k in range(2 * half)], dtype=np.float32)
 
 
 @dataclass(frozen=True)

@@ -16,18 +16,21 @@ products) runs on the device through ltq_amd.linalg and torch, i.e. as large hip
 from __future__ import annotations
 
 import os
+from dataclasses import dataclass
 from typing import Dict, List, Optional, Tuple
 
 import torch
 
 from . import _lib, linalg, rotation
-from .formats import QK_K, SUBBLOCK_SIZE, TCQ_CONFIG
+from .formats import E_BITS, E_STEP, QK_K, SUBBLOCK_SIZE, TCQ_CONFIG, exp2_table
 from .tcq_proto import make_gains, viterbi_ub_cuda
 
 PACK: Optional[dict] = None
 # timing hook (off by default): a list receives (stage name, torch.cuda.Event) at every stage boundary of
 # quantize_matrix_liqk_v2, recorded on the stream the kernels run on
 STAGE_EVENTS: Optional[list] = None
+# the refit record of the last quantize_matrix_liqk_v2 call (for inspection)
+LAST_REFIT = None
 NUM_SUBBLOCKS = QK_K // SUBBLOCK_SIZE
 
 
@@ -68,6 +71,24 @@ def factor_hessian(H_rot: torch.Tensor, damp: float) -> Tuple[torch.Tensor, torc
     return U, diag_w, U_blks_inv
 
 
+_EXP2_TABS: Dict[tuple, torch.Tensor] = {}
+
+
+def exp2_table_device(device, e_step: float = E_STEP, e_bits: int = E_BITS) -> torch.Tensor:
+    """formats.exp2_table on `device` (cached per device and exponent format)."""
+    key = (str(torch.device(device)), float(e_step), int(e_bits))
+    t = _EXP2_TABS.get(key)
+    if t is None:
+        t = _EXP2_TABS[key] = torch.from_numpy(exp2_table(e_step, e_bits)).to(device)
+    return t
+
+
+def block_scale(d_row: torch.Tensor, e: torch.Tensor, e_step: float = E_STEP, e_bits: int = E_BITS) -> torch.Tensor:
+    """d_row[m] * 2^(e_step e[m, b]) [M, nblk] float32 through the shared exponent table (src/liqk_v2.py:946)."""
+    tab = exp2_table_device(d_row.device, e_step, e_bits)
+    return d_row.float().unsqueeze(1) * tab[e.long() + (1 << (e_bits - 1))]
+
+
 @torch.no_grad()
 def row_scale(W_rot: torch.Tensor, cfg: dict) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(d_row [M] fp32 holding fp16 values, e [M, K/256] int8, d [M, K/256] = max(d_row 2^(e_step e), 1e-8))."""
@@ -77,12 +98,14 @@ def row_scale(W_rot: torch.Tensor, cfg: dict) -> Tuple[torch.Tensor, torch.Tenso
         W = W.contiguous()
     M, K = W.shape
     nblk = K // QK_K
+    e_step, e_bits = float(cfg.get("e_step", E_STEP)), int(cfg.get("e_bits", E_BITS))
+    tab = exp2_table_device(W.device, e_step, e_bits)
     d_row = torch.empty(M, dtype=torch.float32, device=W.device)
     e = torch.empty((M, nblk), dtype=torch.int8, device=W.device)
     d = torch.empty((M, nblk), dtype=torch.float32, device=W.device)
-    _check(_lib.lib().ltq_row_scale(W.data_ptr(), M, K, W.stride(0), float(cfg.get("scale", 1.0)),
-                                    float(cfg.get("e_step", 0.25)), int(cfg.get("e_bits", 5)), d_row.data_ptr(),
-                                    e.data_ptr(), nblk, d.data_ptr(), nblk, _lib.stream_ptr()), "ltq_row_scale")
+    _check(_lib.lib().ltq_row_scale(W.data_ptr(), M, K, W.stride(0), float(cfg.get("scale", 1.0)), e_step, e_bits,
+                                    tab.data_ptr(), d_row.data_ptr(), e.data_ptr(), nblk, d.data_ptr(), nblk,
+                                    _lib.stream_ptr()), "ltq_row_scale")
     return d_row, e, d
 
 
@@ -166,134 +189,212 @@ def _quantize_rows_tcq_ldlq(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: to
     return d_full, W_hat_rot
 
 
-def _fwht_rows(X: torch.Tensor) -> torch.Tensor:
-    """Block normalized FWHT-256 along the first dimension."""
-    return rotation.fwht_cols(X.float())
+# ------------------------------------------------------------------------------------------------------------
+# The matrix driver. A matrix job runs in stages: rotation (suh, FWHT) -> factors of the rotated Hessian ->
+# every format's row group through the LDLQ + Viterbi loop -> the joint c_row / suh refit -> the .ltq fields.
+# ------------------------------------------------------------------------------------------------------------
+
+@dataclass
+class RefitResult:
+    """What the joint c_row / suh refit (src/liqk_v2.py:1139-1180) computed, kept for inspection.
+
+    c_raw [M]: per-row least-squares gain <W_hat, W H> / <W_hat, W_hat H> of the pre-refit reconstruction;
+    c_row [M]: c_raw where finite and strictly inside (0.5, 2), else 1; d_new [M, nblk] fp16(d c_row);
+    c_eff [M]: mean over the row's blocks of d_new / d; A (lower triangle, ridge included; only with keep) and
+    b [K]: the normal equations of the column scale; s_solved: the solve's fp32 output (None when the solve
+    failed); suh_cand: fp16(s_solved) where inside (0.05, 10) in magnitude, else the old suh; the two weighted
+    proxy losses and whether the candidate replaced the old scales (strictly lower loss)."""
+    c_raw: torch.Tensor
+    c_row: torch.Tensor
+    d_new: torch.Tensor
+    c_eff: torch.Tensor
+    A: Optional[torch.Tensor]
+    b: torch.Tensor
+    s_solved: Optional[torch.Tensor]
+    suh_cand: torch.Tensor
+    loss_base: float
+    loss_cand: float
+    accepted: bool
+
+
+def row_proxy(HW: torch.Tensor, HQ: torch.Tensor, W: torch.Tensor, W_hat: torch.Tensor) -> torch.Tensor:
+    """[M]: sum_j ((W - W_hat) H)[m, j] (W - W_hat)[m, j], with (W - W_hat) H formed as HW - HQ (no extra
+    M x K x K product)."""
+    return ((HW - HQ) * (W - W_hat)).sum(dim=1)
+
+
+@torch.no_grad()
+def refit_scales(W: torch.Tensor, H: torch.Tensor, HW: torch.Tensor, U_base: torch.Tensor, suh: torch.Tensor,
+                 d: torch.Tensor, rw: Optional[torch.Tensor],
+                 keep: bool = False) -> Tuple[RefitResult, torch.Tensor, torch.Tensor]:
+    """The refit for W [M, K] (fp32), H, HW = W H, U_base = FWHT of the rotated reconstruction (so that the
+    reconstruction is U_base * suh), the per-(row, block) scales d [M, nblk] fp16 and the normalized row weights
+    rw [M] (None: unweighted). Returns (the record, the reconstruction W_hat of the scales the record chose,
+    W_hat H): (c_eff U_base) * suh_cand when accepted, else U_base * suh."""
+    W_hat = U_base * suh.unsqueeze(0)
+    HQ = W_hat @ H
+    gain_num = torch.einsum("mk,mk->m", W_hat, HW)
+    gain_den = torch.einsum("mk,mk->m", W_hat, HQ).clamp(min=1e-12)
+    c_raw = gain_num / gain_den
+    usable = torch.isfinite(c_raw) & (c_raw > 0.5) & (c_raw < 2.0)
+    c_row = torch.where(usable, c_raw, torch.ones_like(c_raw))
+    d32 = d.float()
+    d_new = (d32 * c_row.unsqueeze(1)).to(torch.float16)
+    c_eff = (d_new.float() / d32.clamp(min=1e-12)).mean(dim=1)
+    # the column-scale normal equations (U_w^T U_s) o H s = sum over rows of U_w o HW, U_s = c_eff U_base,
+    # U_w = rw U_s; the matrix is symmetric and only its lower triangle is formed (all the Cholesky reads)
+    U_s = U_base * c_eff.unsqueeze(1)
+    U_w = U_s if rw is None else U_s * rw.unsqueeze(1)
+    A = linalg.gram_lower(U_w, U_s).mul_(H)
+    b = (U_w * HW).sum(dim=0)
+    A.diagonal().add_(1e-3 * A.diagonal().mean().clamp(min=1e-12))
+    weight = torch.ones_like(c_row) if rw is None else rw
+    loss_base = float((row_proxy(HW, HQ, W, W_hat) * weight).sum().item())
+    s_solved, suh_cand, loss_cand, W_cand, HQ_cand = None, suh, float("inf"), None, None
+    try:
+        s_solved = linalg.spd_solve(A, b)
+    except RuntimeError:  # a singular system leaves the scales as they are (src/liqk_v2.py:1179-1180)
+        pass
+    if s_solved is not None:
+        s16 = s_solved.to(torch.float16).to(torch.float32)
+        good = torch.isfinite(s16) & (s16.abs() > 0.05) & (s16.abs() < 10.0)
+        suh_cand = torch.where(good, s16, suh)
+        W_cand = U_s * suh_cand.unsqueeze(0)
+        HQ_cand = W_cand @ H
+        loss_cand = float((row_proxy(HW, HQ_cand, W, W_cand) * weight).sum().item())
+    accepted = loss_cand < loss_base
+    rec = RefitResult(c_raw, c_row, d_new, c_eff, A if keep else None, b, s_solved, suh_cand, loss_base, loss_cand,
+                      accepted)
+    return (rec, W_cand, HQ_cand) if accepted else (rec, W_hat, HQ)
+
+
+def _row_slices(spec_or_row_specs, M: int) -> List[Tuple[int, int, str]]:
+    if isinstance(spec_or_row_specs, str):
+        return [(0, M, spec_or_row_specs)]
+    return [(int(r0), int(r1), sp) for r0, r1, sp in spec_or_row_specs]
+
+
+def _rows_of(row_slices, device) -> Dict[str, torch.Tensor]:
+    """format -> the (sorted by slice order) row indices it quantizes."""
+    groups: Dict[str, List[torch.Tensor]] = {}
+    for r0, r1, sp in row_slices:
+        groups.setdefault(sp, []).append(torch.arange(r0, r1, device=device))
+    return {sp: torch.cat(parts) for sp, parts in groups.items()}
+
+
+class _MatrixJob:
+    """One matrix through the quantizer (src/liqk_v2.py:1030-1198): the stages below share its state."""
+
+    def __init__(self, W, H, row_slices, seed, damp, row_weights):
+        self.W = W.float()
+        self.H = H.float()
+        self.M, self.K = self.W.shape
+        self.nblk = self.K // QK_K
+        self.row_slices = row_slices
+        for _, _, sp in row_slices:
+            if sp not in TCQ_CONFIG:
+                raise NotImplementedError(f"{sp}: only TCQ formats are quantized on the GPU path")
+        # TCQ formats take 10x the damping of the other families (src/liqk_v2.py:1061-1063)
+        self.damp = damp * float(os.environ.get("TCQ_DAMP_MULT", "10"))
+        self.seed = seed
+        self.row_weights = row_weights
+
+    def rotate_and_factor(self):
+        self.W_rot, H_rot, self.suh = rotation.compute_optimal_suh(self.W, self.H, seed=self.seed,
+                                                                   row_weights=self.row_weights)
+        _mark("rotation")
+        self.U, self.diag_w, self.U_blks_inv = factor_hessian(H_rot, self.damp)
+        del H_rot
+        _mark("factor")
+
+    def quantize_groups(self):
+        """Each format's rows through the LDLQ loop; with PACK, the tile fields gathered into matrix order."""
+        dev = self.W.device
+        self.W_hat_rot = torch.empty_like(self.W_rot)
+        self.d = torch.empty((self.M, self.nblk), dtype=torch.float16, device=dev)
+        self.fields = None
+        if PACK is not None:
+            PACK["groups"] = []
+            self.fields = {"idx": torch.empty((self.M, self.K), dtype=torch.int16, device=dev),
+                           "gi": torch.empty((self.M, self.K), dtype=torch.uint8, device=dev),
+                           "G": torch.empty((self.M, self.K), dtype=torch.float32, device=dev),
+                           "d_row": torch.empty(self.M, device=dev),
+                           "e": torch.empty((self.M, self.nblk), dtype=torch.int8, device=dev)}
+        for sp, rows in _rows_of(self.row_slices, dev).items():
+            d_g, W_hat_g = _quantize_rows_tcq_ldlq(self.W_rot[rows], self.U, self.U_blks_inv, self.diag_w, sp)
+            self.W_hat_rot[rows] = W_hat_g
+            self.d[rows] = d_g
+            if self.fields is not None:
+                got = PACK["groups"].pop()
+                for name, dst in self.fields.items():
+                    dst[rows] = got[name].to(dst.dtype)
+        _mark("rows")
+
+    def refit(self):
+        self.HW = self.W @ self.H
+        U_base = rotation.fwht_inplace(self.W_hat_rot, block_size=QK_K)
+        rw = None
+        if self.row_weights is not None:
+            rw = rotation.normalized_row_weights(self.row_weights.to(self.W.device)).float()
+        rec, self.W_hat, self.HQ = refit_scales(self.W, self.H, self.HW, U_base, self.suh, self.d, rw)
+        global LAST_REFIT
+        LAST_REFIT = rec
+        self.c_pack = torch.ones(self.M, device=self.W.device)
+        if rec.accepted:
+            self.suh, self.d, self.c_pack = rec.suh_cand, rec.d_new, rec.c_eff
+
+    def write_fields(self):
+        """PACK["matrix"]: the .ltq fields, and the reconstruction the file decodes to (src/liqk_v2.py:1182-1190).
+        The decoded matrix equals the refit's reconstruction with row m scaled by rho_m = fp16(d_row c) /
+        (d_row c) (same tile values and fp16 suh), so W_hat H is the refit's HQ scaled by row; rows whose block
+        scale met the 1e-8 clamp are multiplied out."""
+        f = self.fields
+        d_row_file = (f["d_row"] * self.c_pack).to(torch.float16)
+        suh_file = self.suh.to(torch.float16)
+        scale = block_scale(d_row_file, f["e"])
+        W_rot_file = (scale.unsqueeze(2) * f["G"].view(self.M, self.nblk, QK_K)).view(self.M, self.K)
+        self.W_hat = rotation.fwht_inplace(W_rot_file, block_size=QK_K) * suh_file.float().unsqueeze(0)
+        rho = d_row_file.float() / (f["d_row"] * self.c_pack)
+        self.HQ = self.HQ * rho.unsqueeze(1)
+        clamped = (block_scale(f["d_row"], f["e"]) < 1e-8).any(dim=1)
+        if bool(clamped.any()):
+            self.HQ[clamped] = self.W_hat[clamped] @ self.H
+        PACK["matrix"] = {"row_slices": self.row_slices, "idx": f["idx"], "gi": f["gi"], "G": f["G"],
+                          "d_row": d_row_file, "e": f["e"], "suh": suh_file}
+
+    def relative_loss(self) -> float:
+        num = float(row_proxy(self.HW, self.HQ, self.W, self.W_hat).sum().item())
+        den = float(torch.einsum("mk,mk->", self.HW, self.W).clamp(min=1e-12).item())
+        return num / den
 
 
 @torch.no_grad()
 def quantize_matrix_liqk_v2(W: torch.Tensor, H: torch.Tensor, spec_or_row_specs, seed: int = 1337, damp: float = 0.02,
                             row_weights: Optional[torch.Tensor] = None, cd_sweeps: int = 2,
                             out_rot: bool = False) -> Tuple[Dict[str, torch.Tensor], torch.Tensor, float]:
-    """W [M, K] with input Hessian H [K, K] -> (qdata {d, suh, row_slices}, W_hat_eff, relative proxy loss),
-    for TCQ specs (one for the whole matrix or [(r0, r1, spec), ...] row slices)."""
+    """W [M, K] with input Hessian H [K, K] -> (qdata {d, suh, row_slices[, s_out]}, W_hat [M, K], relative proxy
+    loss tr(dW H dW^T) / tr(W H W^T)) for one TCQ format or row slices [(r0, r1, format), ...]
+    (src/liqk_v2.py:1030-1198; cd_sweeps is accepted and unused, as there). With out_rot the rows are first
+    rotated by a block FWHT-256 with Rademacher signs s_out (seed + 7919); row weights are then averaged per
+    256 rows, and the result is rotated back."""
+    s_out = None
     if out_rot:
         s_out = rotation.make_rademacher_signs(W.shape[0], seed=seed + 7919, device=W.device)
-        rw = None
+        W = rotation.fwht_cols(W.float(), s_out, mode=2)
         if row_weights is not None:
-            rw = row_weights.float().view(-1, QK_K).mean(dim=1, keepdim=True).expand(-1, QK_K).reshape(-1)
-        q_res, w_hat_r, rel = quantize_matrix_liqk_v2(_fwht_rows(W.float() * s_out.unsqueeze(1)), H, spec_or_row_specs,
-                                                      seed=seed, damp=damp, row_weights=rw, cd_sweeps=cd_sweeps)
-        q_res["s_out"] = s_out.to(torch.int8)
-        return q_res, _fwht_rows(w_hat_r) * s_out.unsqueeze(1), rel
-
-    W_f32 = W.float()
-    H_f32 = H.float()
-    M, K = W_f32.shape
-    nblocks = K // QK_K
-    specs_used = [spec_or_row_specs] if isinstance(spec_or_row_specs, str) else [sp for _, _, sp in spec_or_row_specs]
-    for sp in specs_used:
-        if sp not in TCQ_CONFIG:
-            raise NotImplementedError(f"{sp}: only TCQ formats are quantized on the GPU path")
-    damp *= float(os.environ.get("TCQ_DAMP_MULT", "10"))
-
+            row_weights = row_weights.float().view(-1, QK_K).mean(dim=1).repeat_interleave(QK_K)
     _mark("start")
-    W_rot, H_rot, suh = rotation.compute_optimal_suh(W_f32, H_f32, seed=seed, row_weights=row_weights)
-    _mark("rotation")
-    U, diag_w, U_blks_inv = factor_hessian(H_rot, damp)
-    del H_rot
-    _mark("factor")
-
-    row_slices = [(0, M, spec_or_row_specs)] if isinstance(spec_or_row_specs, str) else spec_or_row_specs
-    by_spec: Dict[str, List[Tuple[int, int]]] = {}
-    for r0, r1, sp in row_slices:
-        by_spec.setdefault(sp, []).append((r0, r1))
-
-    W_hat_rot = torch.empty_like(W_rot)
-    d_full = torch.empty((M, nblocks), dtype=torch.float16, device=W.device)
-    if PACK is not None:
-        PACK["groups"] = []
-        pm = {"idx": torch.empty((M, K), dtype=torch.int16, device=W.device),
-              "gi": torch.empty((M, K), dtype=torch.uint8, device=W.device),
-              "G": torch.empty((M, K), dtype=torch.float32, device=W.device),
-              "d_row": torch.empty(M, device=W.device),
-              "e": torch.empty((M, nblocks), dtype=torch.int8, device=W.device)}
-    for sp, ranges in by_spec.items():
-        rows_idx = torch.cat([torch.arange(r0, r1, device=W.device) for r0, r1 in ranges], dim=0)
-        d_sub, Wh_sub = _quantize_rows_tcq_ldlq(W_rot[rows_idx], U, U_blks_inv, diag_w, sp)
-        W_hat_rot[rows_idx] = Wh_sub
-        d_full[rows_idx] = d_sub
-        if PACK is not None:
-            g = PACK["groups"].pop()
-            for k in ("idx", "gi", "G", "d_row", "e"):
-                pm[k][rows_idx] = g[k].to(pm[k].dtype)
-    _mark("rows")
-
-    # ---- c_row / suh refit (src/liqk_v2.py:1139-1180) ----------------------------------------------------
-    U_base = rotation.fwht_inplace(W_hat_rot.clone(), block_size=QK_K)
-    W_hat_eff = U_base * suh.unsqueeze(0)
-    c_pack = torch.ones((M,), dtype=torch.float32, device=W.device)
-    HW = W_f32 @ H_f32
-    HQ = W_hat_eff @ H_f32
-    c_row = (W_hat_eff * HW).sum(dim=1) / (W_hat_eff * HQ).sum(dim=1).clamp(min=1e-12)
-    c_row = torch.where(torch.isfinite(c_row) & (c_row > 0.5) & (c_row < 2.0), c_row, torch.ones_like(c_row))
-    d_new = (d_full.float() * c_row.unsqueeze(1)).to(torch.float16)
-    c_eff = (d_new.float() / d_full.float().clamp(min=1e-12)).mean(dim=1, keepdim=True)
-    U_scaled = U_base * c_eff
-    if row_weights is not None:
-        rw = row_weights.float().clamp(min=float(row_weights.mean().item()) * 0.1)
-        rw = (rw / rw.mean().clamp(min=1e-12)).clamp(0.25, 4.0)
-        U_w = U_scaled * rw.unsqueeze(1)
-    else:
-        rw = torch.ones((M,), dtype=torch.float32, device=W.device)
-        U_w = U_scaled
-    # A_in = (U_w^T U_scaled) * H is symmetric (U_w = diag(rw) U_scaled): only its lower triangle is formed, which
-    # is all the Cholesky of spd_solve reads
-    A_in = linalg.gram_lower(U_w, U_scaled).mul_(H_f32)
-    b_in = (U_w * HW).sum(dim=0)
-    A_in.diagonal().add_(1e-3 * A_in.diagonal().mean().clamp(min=1e-12))
-    try:
-        suh_cand = linalg.spd_solve(A_in, b_in).to(torch.float16).to(torch.float32)
-        valid_s = torch.isfinite(suh_cand) & (suh_cand.abs() > 0.05) & (suh_cand.abs() < 10.0)
-        suh_cand = torch.where(valid_s, suh_cand, suh)
-        W_hat_cand = U_scaled * suh_cand.unsqueeze(0)
-        HQ_cand = W_hat_cand @ H_f32
-        diff_base = W_f32 - W_hat_eff
-        diff_cand = W_f32 - W_hat_cand
-        loss_base = float((((HW - HQ) * diff_base).sum(dim=1) * rw).sum().item())
-        loss_cand = float((((HW - HQ_cand) * diff_cand).sum(dim=1) * rw).sum().item())
-        if loss_cand < loss_base:
-            W_hat_eff = W_hat_cand
-            d_full = d_new
-            suh = suh_cand
-            HQ = HQ_cand
-            c_pack = c_eff.squeeze(1)
-    except RuntimeError:
-        pass
-    del A_in
-
-    if PACK is not None:  # the matrix exactly from the file fields
-        d_row_p = (pm["d_row"] * c_pack).to(torch.float16)
-        suh_p = suh.to(torch.float16)
-        scale = d_row_p.float().unsqueeze(1) * torch.exp2(0.25 * pm["e"].float())
-        Wq_rot = (scale.unsqueeze(2) * pm["G"].view(M, nblocks, QK_K)).view(M, K)
-        W_hat_eff = rotation.fwht_inplace(Wq_rot, block_size=QK_K) * suh_p.float().unsqueeze(0)
-        # the rebuilt matrix is the refit's W_hat_eff with row r scaled by rho_r = d_row_p / (d_row c_pack) (same
-        # tile values, same fp16 suh), so its product with H is HQ scaled by row, equal to the reference's
-        # W_hat_eff @ H up to fp32 rounding; rows whose block scale hit the 1e-8 clamp of the row-scale fit (where
-        # the identity does not hold) are multiplied out
-        rho = d_row_p.float() / (pm["d_row"] * c_pack)
-        HQ = HQ * rho.unsqueeze(1)
-        clamped = ((pm["d_row"].unsqueeze(1) * torch.exp2(0.25 * pm["e"].float())) < 1e-8).any(dim=1)
-        if bool(clamped.any()):
-            HQ[clamped] = W_hat_eff[clamped] @ H_f32
-        PACK["matrix"] = {"row_slices": row_slices, "idx": pm["idx"], "gi": pm["gi"], "G": pm["G"], "d_row": d_row_p,
-                          "e": pm["e"], "suh": suh_p}
-
-    diff = W_f32 - W_hat_eff
-    num_loss = float(((HW - HQ) * diff).sum().item())
-    den_loss = float((HW * W_f32).sum().clamp(min=1e-12).item())
-    rel_loss = num_loss / den_loss
-    qdata_out = {"d": d_full, "suh": suh.to(torch.float16), "row_slices": row_slices}
+    job = _MatrixJob(W, H, _row_slices(spec_or_row_specs, W.shape[0]), seed, damp, row_weights)
+    job.rotate_and_factor()
+    job.quantize_groups()
+    job.refit()
+    if job.fields is not None:
+        job.write_fields()
+    rel = job.relative_loss()
+    q = {"d": job.d, "suh": job.suh.to(torch.float16), "row_slices": job.row_slices}
+    W_hat = job.W_hat
+    if s_out is not None:
+        q["s_out"] = s_out.to(torch.int8)
+        W_hat = rotation.fwht_cols(W_hat) * s_out.unsqueeze(1)
     _mark("refit")
-    return qdata_out, W_hat_eff, rel_loss
+    return q, W_hat, rel

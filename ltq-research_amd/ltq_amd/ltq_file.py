@@ -1,18 +1,25 @@
 """The .ltq container of the quantizer's PACK output: tile packing and decoding on the GPU, file writing and
 reading on the host.
 
-Mirrors src/ltq_file.py (same names, arguments and file layout):
+Same names, arguments and file bytes as src/ltq_file.py:
   pack_slice / pack_slice_device   :79-96   four structure-of-arrays regions (codes, uncoded bit planes, lowest
                                              uncoded bit, gain indices), each on a 64-byte boundary, tiles by row
                                              group then 16-column block (position t = 16 r + c); HIP ltq_pack_slice
   decode_slice                     :119-147 the spec decoder; HIP ltq_unpack_slice
   assemble                         :150-156 W = H256(d q) * suh, d[m, b] = d_row[m] 2^(e[m, b] / 4)
   format_json / format_from_json   :40-50   the header's format description (lut and gains as exact floats)
-  LtqWriter                        :163-225 data after a reserved header of 16 + reserve bytes (4096-aligned),
-                                             tensors 64-byte aligned, add_matrix (with decode verification) and
-                                             finalize (magic, version, reserve, space-padded JSON header)
-  LtqFile                          :248-280 header parse, memory-mapped tensors, decode_matrix
+  LtqWriter                        :163-225 writer: data region behind a reserved header, 64-byte aligned tensors,
+                                             add_matrix with decode verification, finalize
+  LtqFile                          :248-280 reader: header, memory-mapped tensors, decode_matrix
 Ring records (rows of row tables): pack_rings_device, ring_bytes (src/ltq_format.py:42-50, 104-124).
+
+File layout (a format, kept byte for byte): a 16-byte preamble (b"LTQ\0", uint32 version 1, uint64 header
+reserve R, little endian), the UTF-8 JSON header (compact separators) space-padded to R bytes, then the data
+region at 16 + R, a multiple of 4096. The header's "tensors" maps each name to {"dtype", "shape", "offset"}, the
+offset relative to the data region and a multiple of 64; alignment gaps are zero bytes. A matrix p is five
+tensors: p.ltq.slices (int32 [n, 4]: r0, r1, format index, byte offset in p.ltq.data), p.ltq.data (u8, the
+packed row slices, each on a 64-byte boundary of the blob), p.ltq.d_row (f16 [M]), p.ltq.e (i8 [M, K / 256]) and
+p.ltq.suh (f16 [K]).
 """
 from __future__ import annotations
 
@@ -24,31 +31,44 @@ import numpy as np
 import torch
 
 from . import _lib
-from .formats import LtqFormat
+from .formats import E_BITS, E_STEP, LtqFormat, exp2_table
 
 MAGIC = b"LTQ\0"
 VERSION = 1
 TILE = 256
-DTYPES = {"f32": (np.float32, torch.float32), "f16": (np.float16, torch.float16), "bf16": (np.uint16, torch.bfloat16),
-          "i32": (np.int32, torch.int32), "i8": (np.int8, torch.int8), "u8": (np.uint8, torch.uint8)}
-TORCH_TO_LTQ = {v[1]: k for k, v in DTYPES.items()}
-FRAC_NAMES = ["none", "d2", "d4"]
+_PREAMBLE = struct.Struct("<4sIQ")
+_DATA_ALIGN, _TENSOR_ALIGN = 4096, 64
+
+# dtype code -> (element type of the stored bytes, torch dtype); bf16 is stored as its 16-bit pattern
+DTYPES = {code: (np.dtype(npt), tt) for code, npt, tt in (
+    ("f32", np.float32, torch.float32), ("f16", np.float16, torch.float16), ("bf16", np.uint16, torch.bfloat16),
+    ("i32", np.int32, torch.int32), ("i8", np.int8, torch.int8), ("u8", np.uint8, torch.uint8))}
+TORCH_TO_LTQ = {tt: code for code, (_, tt) in DTYPES.items()}
+FRAC_NAMES = ("none", "d2", "d4")
 
 
-def _align(x: int, a: int) -> int:
-    return (x + a - 1) // a * a
+def _round_up(n: int, a: int) -> int:
+    return -(-n // a) * a
+
+
+def _f32_list(a) -> list:
+    """float32 values as Python floats (each float32 converts to a double exactly, so the JSON text names it
+    uniquely and reads back to the same bits)."""
+    return np.asarray(a, np.float32).astype(np.float64).tolist()
 
 
 def format_json(f: LtqFormat) -> dict:
-    """Header description of a format; lut and gains as float32 values written exactly (repr of each float32)."""
-    return {"name": f.name, "K": f.K, "frac": FRAC_NAMES[f.frac], "masks": [int(m) for m in f.masks], "h": f.h,
-            "sub": f.sub, "lut": [float(v) for v in np.asarray(f.lut, np.float32)],
-            "gain": [float(v) for v in np.asarray(f.gain_tab, np.float32)]}
+    """Header description of a format (key order is part of the file bytes)."""
+    d = dict(name=f.name, K=f.K, frac=FRAC_NAMES[f.frac], masks=[int(m) for m in f.masks], h=f.h, sub=f.sub)
+    d["lut"], d["gain"] = _f32_list(f.lut), _f32_list(f.gain_tab)
+    return d
 
 
 def format_from_json(d: dict) -> LtqFormat:
-    return LtqFormat(d["name"], d["K"], FRAC_NAMES.index(d["frac"]), tuple(d["masks"]), d["h"], 0.0, d["sub"],
-                     np.asarray(d["lut"], np.float32), np.asarray(d["gain"], np.float32))
+    """LtqFormat of a header description (the gain step is not stored: the gain table is)."""
+    return LtqFormat(name=d["name"], K=int(d["K"]), frac=FRAC_NAMES.index(d["frac"]), masks=tuple(d["masks"]),
+                     h=int(d["h"]), step=0.0, sub=int(d["sub"]), lut=np.asarray(d["lut"], np.float32),
+                     gain_tab=np.asarray(d["gain"], np.float32))
 
 
 def slice_bytes(R: int, K: int, f: LtqFormat) -> int:
@@ -137,111 +157,142 @@ def decode_slice(data, R: int, K: int, f: LtqFormat, device) -> torch.Tensor:
 
 @torch.no_grad()
 def assemble(G: torch.Tensor, d_row: torch.Tensor, e: torch.Tensor, suh: torch.Tensor) -> torch.Tensor:
-    """W = H256(d q) * suh over columns, d[m, b] = d_row[m] 2^(e[m, b] / 4) (src/ltq_file.py:150-156)."""
+    """W [M, K] = H256(d q) * suh over columns with d[m, b] = d_row[m] 2^(e[m, b] / 4) (src/ltq_file.py:150-156);
+    the block factor is read from the shared exponent table (formats.exp2_table), as the quantizer's row scale
+    reads it."""
     from . import rotation
     M, K = G.shape
-    scale = d_row.float().unsqueeze(1) * torch.exp2(0.25 * e.float())
-    W = (scale.unsqueeze(2) * G.view(M, K // TILE, TILE)).view(M, K)
-    return rotation.fwht_inplace(W, block_size=TILE) * suh.float().unsqueeze(0)
+    tab = torch.from_numpy(exp2_table(E_STEP, E_BITS)).to(G.device)
+    scale = d_row.float().unsqueeze(1) * tab[e.long() + (1 << (E_BITS - 1))]
+    Wq = (G.float().view(M, K // TILE, TILE) * scale.unsqueeze(2)).view(M, K)
+    return rotation.fwht_inplace(Wq, block_size=TILE) * suh.float().unsqueeze(0)
+
+
+def _host_bytes(t: torch.Tensor):
+    """(dtype code, shape, raw bytes) of a tensor as the file stores it."""
+    t = t.detach().to("cpu").contiguous()
+    code = TORCH_TO_LTQ[t.dtype]
+    arr = t.view(torch.int16).numpy() if t.dtype == torch.bfloat16 else t.numpy()
+    return code, list(t.shape), arr.tobytes()
 
 
 class LtqWriter:
-    """Writes tensors straight to the file behind a reserved header (data starts at 16 + reserve, a multiple of
-    4096); `finalize` writes magic, version, reserve and the JSON header, space-padded to the reserve."""
+    """Streams tensors into the data region of a new .ltq file; finalize(header) writes the preamble and the
+    header into the reserved space. `tensors` is the catalog the header will carry, `quantized` the matrices
+    added with add_matrix."""
 
     def __init__(self, path, formats, reserve: int = (64 << 20) - 16):
-        assert (16 + reserve) % 4096 == 0
-        self.path, self.reserve = Path(path), reserve
+        if (_PREAMBLE.size + reserve) % _DATA_ALIGN:
+            raise AssertionError(f"the data region must start on a {_DATA_ALIGN}-byte boundary (reserve {reserve})")
+        self.path, self.reserve = Path(path), int(reserve)
         self.formats = list(formats)
         self.fmt_index = {f.name: i for i, f in enumerate(self.formats)}
-        self.f = open(self.path, "wb")
-        self.f.write(bytes(16 + reserve))
-        self.cur = 0
-        self.tensors = {}
-        self.quantized = []
+        self.tensors: dict = {}
+        self.quantized: list = []
+        self._base = _PREAMBLE.size + self.reserve
+        self._used = 0
+        self._fh = open(self.path, "wb")
+        self._fh.truncate(self._base)  # the reserved header space reads as zeros until finalize
 
-    def _write(self, name: str, raw: bytes, dtype: str, shape, align: int = 64):
-        pad = _align(self.cur, align) - self.cur
-        if pad:
-            self.f.write(bytes(pad))
-            self.cur += pad
-        self.tensors[name] = {"dtype": dtype, "shape": [int(v) for v in shape], "offset": self.cur}
-        self.f.write(raw)
-        self.cur += len(raw)
+    def _place(self, name: str, code: str, shape, payload) -> int:
+        off = _round_up(self._used, _TENSOR_ALIGN)
+        self._fh.seek(self._base + self._used)
+        self._fh.write(bytes(off - self._used))
+        self._fh.write(payload)
+        self._used = off + len(payload)
+        self.tensors[name] = {"dtype": code, "shape": [int(v) for v in shape], "offset": off}
+        return off
 
     def add_tensor(self, name: str, t: torch.Tensor):
-        t = t.detach().cpu().contiguous()
-        dt = TORCH_TO_LTQ[t.dtype]
-        raw = t.view(torch.int16).numpy().tobytes() if t.dtype == torch.bfloat16 else t.numpy().tobytes()
-        self._write(name, raw, dt, list(t.shape))
+        self._place(name, *_host_bytes(t))
 
     def add_matrix(self, p: str, m: dict, verify: bool = True) -> int:
-        """A matrix from PACK["matrix"] of the quantizer; returns the byte size of its fields. With verify, each
-        slice decoded from the written bytes must equal the quantizer's tile values G bit for bit."""
+        """Writes PACK["matrix"] of the quantizer as the five tensors of matrix p; returns their payload bytes.
+        The row slices are packed on the device into one blob; with verify, the spec decoder reads every slice
+        back from the packed bytes and must give the quantizer's tile values G bit for bit."""
         M, K = m["idx"].shape
-        rows, data = [], bytearray()
+        table, chunks, used = [], [], 0
         for r0, r1, sp in m["row_slices"]:
-            f = self.formats[self.fmt_index[sp]]
-            data += bytes(_align(len(data), 64) - len(data))
-            rows.append([r0, r1, self.fmt_index[sp], len(data)])
-            dev_bytes = pack_slice_device(m["idx"][r0:r1], m["gi"][r0:r1], f)
+            fi = self.fmt_index[sp]
+            f = self.formats[fi]
+            packed = pack_slice_device(m["idx"][r0:r1], m["gi"][r0:r1], f)
             if verify:
-                G = m["G"][r0:r1]
-                dec = decode_slice(dev_bytes, r1 - r0, K, f, G.device)
-                bad = int((dec.view(torch.int32) != G.float().contiguous().view(torch.int32)).sum())
-                if bad:
-                    raise RuntimeError(f"{p} [{r0}:{r1}] {sp}: decode disagrees with the quantizer in {bad} weights")
-            data += bytes(dev_bytes.cpu().numpy().tobytes())
-        self.add_tensor(f"{p}.ltq.slices", torch.tensor(rows, dtype=torch.int32))
-        self._write(f"{p}.ltq.data", bytes(data), "u8", [len(data)])
+                dec = decode_slice(packed, r1 - r0, K, f, packed.device)
+                want = m["G"][r0:r1].float().contiguous()
+                n_bad = int((dec.view(torch.int32) != want.view(torch.int32)).sum())
+                if n_bad:
+                    raise RuntimeError(f"{p} [{r0}:{r1}] {sp}: decode disagrees with the quantizer in {n_bad} weights")
+            start = _round_up(used, _TENSOR_ALIGN)
+            if start > used:
+                chunks.append(torch.zeros(start - used, dtype=torch.uint8, device=packed.device))
+            chunks.append(packed)
+            table.append([r0, r1, fi, start])
+            used = start + packed.numel()
+        blob = torch.cat(chunks).cpu().numpy().tobytes() if chunks else b""
+        self.add_tensor(f"{p}.ltq.slices", torch.tensor(table, dtype=torch.int32))
+        self._place(f"{p}.ltq.data", "u8", [len(blob)], blob)
         self.add_tensor(f"{p}.ltq.d_row", m["d_row"].to(torch.float16))
         self.add_tensor(f"{p}.ltq.e", m["e"].to(torch.int8))
         self.add_tensor(f"{p}.ltq.suh", m["suh"].to(torch.float16))
         self.quantized.append(p)
-        return len(data) + 16 * len(rows) + 2 * M + M * (K // TILE) + 2 * K
+        return len(blob) + 16 * len(table) + 2 * M + M * (K // TILE) + 2 * K
 
     def finalize(self, header: dict):
-        header = dict(header, tensors=self.tensors)
-        raw = json.dumps(header, ensure_ascii=False, separators=(",", ":")).encode("utf-8")
-        assert len(raw) <= self.reserve, f"header of {len(raw)} B does not fit in the {self.reserve} B reserve"
-        self.f.seek(0)
-        self.f.write(MAGIC + struct.pack("<IQ", VERSION, self.reserve) + raw + b" " * (self.reserve - len(raw)))
-        self.f.close()
+        body = {**header, "tensors": self.tensors}
+        text = json.dumps(body, ensure_ascii=False, separators=(",", ":")).encode("utf-8")
+        if len(text) > self.reserve:
+            raise AssertionError(f"header of {len(text)} B does not fit in the {self.reserve} B reserve")
+        self._fh.seek(0)
+        self._fh.write(_PREAMBLE.pack(MAGIC, VERSION, self.reserve))
+        self._fh.write(text.ljust(self.reserve, b" "))
+        self._fh.close()
 
 
 class LtqFile:
-    """Reader: header, memory-mapped tensors and the full decode of a matrix."""
+    """Reader of an .ltq file: the parsed header, its formats, tensors mapped from the file, full matrix decode."""
 
     def __init__(self, path):
-        with open(path, "rb") as fh:
-            magic, (ver, H) = fh.read(4), struct.unpack("<IQ", fh.read(12))
-            if magic != MAGIC or ver != VERSION:
-                raise ValueError(f"{path}: not an .ltq v{VERSION} file ({magic!r}, version {ver})")
-            self.header = json.loads(fh.read(H).decode("utf-8"))
-        self.data_off = 16 + H
-        if self.data_off % 4096:
-            raise ValueError(f"{path}: data offset {self.data_off} is not 4096-aligned")
-        self.mm = np.memmap(path, dtype=np.uint8, mode="r")
+        self.path = Path(path)
+        with open(self.path, "rb") as fh:
+            pre = fh.read(_PREAMBLE.size)
+            if len(pre) < _PREAMBLE.size:
+                raise ValueError(f"{path}: too short for an .ltq preamble")
+            magic, version, reserve = _PREAMBLE.unpack(pre)
+            if magic != MAGIC or version != VERSION:
+                raise ValueError(f"{path}: not an .ltq v{VERSION} file ({magic!r}, version {version})")
+            self.header = json.loads(fh.read(reserve).decode("utf-8"))
+        self.data_off = _PREAMBLE.size + reserve
+        if self.data_off % _DATA_ALIGN:
+            raise ValueError(f"{path}: data region at {self.data_off} is not {_DATA_ALIGN}-byte aligned")
+        self.mm = np.memmap(self.path, dtype=np.uint8, mode="r")
         self.formats = [format_from_json(d) for d in self.header["quantization"]["formats"]]
 
-    def raw(self, name: str) -> memoryview:
+    def _entry(self, name: str):
         t = self.header["tensors"][name]
-        n = int(np.prod(t["shape"])) * np.dtype(DTYPES[t["dtype"]][0]).itemsize
-        o = self.data_off + t["offset"]
-        return memoryview(self.mm[o:o + n])
+        np_t, torch_t = DTYPES[t["dtype"]]
+        n = int(np.prod(t["shape"], dtype=np.int64)) * np_t.itemsize
+        lo = self.data_off + int(t["offset"])
+        return t, np_t, torch_t, lo, n
+
+    def raw(self, name: str) -> memoryview:
+        _, _, _, lo, n = self._entry(name)
+        return memoryview(self.mm[lo:lo + n])
 
     def tensor(self, name: str) -> torch.Tensor:
-        t = self.header["tensors"][name]
-        np_dt, _ = DTYPES[t["dtype"]]
-        arr = torch.from_numpy(np.frombuffer(self.raw(name), dtype=np_dt).copy()).reshape(t["shape"])
-        return arr.view(torch.bfloat16) if t["dtype"] == "bf16" else arr
+        t, np_t, torch_t, lo, n = self._entry(name)
+        arr = np.array(self.mm[lo:lo + n]).view(np_t).reshape(t["shape"])
+        out = torch.from_numpy(arr)
+        return out.view(torch.bfloat16) if torch_t == torch.bfloat16 else out
 
     def decode_matrix(self, p: str, device="cuda") -> torch.Tensor:
-        """The matrix W [M, K] float32, as an engine reconstructs it."""
-        d_row, e, suh = (self.tensor(f"{p}.ltq.{k}").to(device) for k in ("d_row", "e", "suh"))
+        """W [M, K] float32 as an engine reconstructs it from the file: every row slice decoded by the spec
+        decoder, then assemble."""
+        d_row = self.tensor(f"{p}.ltq.d_row").to(device)
+        e = self.tensor(f"{p}.ltq.e").to(device)
+        suh = self.tensor(f"{p}.ltq.suh").to(device)
         M, K = d_row.shape[0], suh.shape[0]
-        data = self.raw(f"{p}.ltq.data")
-        G = torch.empty((M, K), device=device)
+        blob = self.raw(f"{p}.ltq.data")
+        G = torch.empty((M, K), dtype=torch.float32, device=device)
         for r0, r1, fi, off in self.tensor(f"{p}.ltq.slices").tolist():
-            G[r0:r1] = decode_slice(data[off:], r1 - r0, K, self.formats[fi], device)
+            G[r0:r1] = decode_slice(blob[off:], r1 - r0, K, self.formats[fi], device)
         return assemble(G, d_row, e, suh)

@@ -99,27 +99,49 @@ def _fwht_rows(X: torch.Tensor) -> torch.Tensor:
     return fwht_cols(X.float())
 
 
+def normalized_row_weights(row_weights: torch.Tensor) -> torch.Tensor:
+    """The row-weight normalization of src/liqk_v2.py:423-425 / :1150-1152 (floor at a tenth of the mean,
+    unit mean, clamp to [0.25, 4]), evaluated in float64."""
+    rw = row_weights.double()
+    rw = rw.clamp(min=float(rw.mean().item()) * 0.1)
+    return (rw / rw.mean().clamp(min=1e-12)).clamp(0.25, 4.0)
+
+
+@torch.no_grad()
+def column_sumsq(W: torch.Tensor, rw: Optional[torch.Tensor] = None, chunk: int = 1024) -> torch.Tensor:
+    """float64 [K]: sum over rows of W^2 (times the row weight), every square exact in float64; row chunks keep
+    the float64 temporary small."""
+    M, K = W.shape
+    acc = torch.zeros(K, dtype=torch.float64, device=W.device)
+    for r0 in range(0, M, chunk):
+        blk = W[r0:r0 + chunk].double().square_()
+        if rw is not None:
+            blk.mul_(rw[r0:r0 + chunk].unsqueeze(1))
+        acc += blk.sum(dim=0)
+    return acc
+
+
 @torch.no_grad()
 def compute_optimal_suh(W: torch.Tensor, H: torch.Tensor, seed: int = 1337,
                         row_weights: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(W_rot, H_rot, suh): suh = fp16(signs * clamp(col_rms^0.5 * h_std^-0.25, 0.25, 4)),
-    W_rot = FWHT_rows(W / suh), H_rot = FWHT_cols(FWHT_rows(H * suh) * suh)."""
+    W_rot = FWHT_rows(W / suh), H_rot = FWHT_cols(FWHT_rows(H * suh) * suh).
+
+    The scale vector is evaluated in float64 from exact squares (the reference's fp32 column reduction and
+    powers, src/liqk_v2.py:419-434, depend on the device's summation order): suh is the fp16 rounding of the
+    scale's exact value except within ~1e-13 of an fp16 rounding boundary, so a CPU restatement gets the same
+    bits."""
     device = W.device
     M, K = W.shape
     signs = make_rademacher_signs(K, seed=seed, device=device)
-    Wf = W.float()
-    if row_weights is not None:
-        rw = row_weights.float().clamp(min=float(row_weights.mean().item()) * 0.1)
-        rw = (rw / rw.mean().clamp(min=1e-12)).clamp(0.25, 4.0)
-        col_rms = ((Wf.square() * rw.unsqueeze(1)).mean(dim=0)).sqrt().clamp(min=1e-6)
-    else:
-        col_rms = Wf.square().mean(dim=0).sqrt().clamp(min=1e-6)
+    rw = normalized_row_weights(row_weights.to(device)) if row_weights is not None else None
+    col_rms = (column_sumsq(W, rw) / M).sqrt().clamp(min=1e-6)
     col_rms = col_rms / col_rms.mean().clamp(min=1e-6)
-    h_std = torch.diagonal(H.float()).clamp(min=1e-8).sqrt()
+    h_std = torch.diagonal(H).double().clamp(min=1e-8).sqrt()
     h_std = h_std / h_std.mean().clamp(min=1e-6)
-    scale = ((col_rms ** 0.5) * (h_std ** -0.25)).clamp(0.25, 4.0)
-    suh = (signs * scale).to(torch.float16).to(torch.float32)
-    W_rot = fwht_rows(W if W.dtype in _DT else Wf, suh, mode=1)
+    scale = (col_rms.sqrt() * h_std.pow(-0.25)).clamp(0.25, 4.0)
+    suh = (signs.double() * scale).to(torch.float16).to(torch.float32)
+    W_rot = fwht_rows(W if W.dtype in _DT else W.float(), suh, mode=1)
     H_tmp = fwht_rows(H.float(), suh, mode=2)
     H_rot = fwht_cols(H_tmp, suh, mode=2, out=H_tmp)
     return W_rot, H_rot, suh

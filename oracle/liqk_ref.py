@@ -2,12 +2,17 @@
 for ltq_amd.liqk). Only tests/ import it.
 
 Reference anchors (torch on the CPU, float32, the reference's order of operations):
-  row_scale_ref          src/liqk_v2.py:938-946
+  row_scale_ref          src/liqk_v2.py:938-946 (the quantizer's bit-exact definition; row_scale_torch_fp32 is
+                         the reference's torch text, kept to count rounding-boundary flips against it)
+  suh_ref                src/liqk_v2.py:409-441 (scale vector in float64; suh_torch_fp32 is the reference's
+                         fp32 torch text, kept to count fp16 flips against it)
   factor_hessian_ref     src/liqk_v2.py:1066-1088
   quantize_rows_ref      src/liqk_v2.py:877-1021, row-scale branch with tail-biting formats (quant_sub at
                          :913-921 via the C oracle's two-pass tail-biting driver)
 """
 from __future__ import annotations
+
+import math
 
 import numpy as np
 import torch
@@ -18,7 +23,61 @@ QK_K = 256
 SUB = 16
 
 
-def row_scale_ref(W_rot: torch.Tensor, cfg: dict):
+def _exp2_table(e_step: float, e_bits: int) -> np.ndarray:
+    """2^(e_step (k - 2^(e_bits-1))) for k < 2^e_bits, float64 rounded once to float32: the block-exponent
+    factors (src/liqk_v2.py:946 evaluates torch.exp2 on them; the values agree, checked in tests)."""
+    half = 1 << (e_bits - 1)
+    return np.array([2.0 ** (e_step * (k - half)) for k in range(2 * half)], np.float32)
+
+
+def block_rms_ref(W_rot: np.ndarray, scale: float) -> np.ndarray:
+    """[M, K/256] fp32: max(sqrt(s / 256), 1e-10) * scale with the block sum of squares s in a fixed order:
+    the 4 squares of each of 64 groups of consecutive elements summed left to right, then a butterfly over
+    group offsets 32, 16, 8, 4, 2, 1 (p_l + p_(l ^ o)). src/liqk_v2.py:941 (`square().mean(2).sqrt()`)."""
+    M, K = W_rot.shape
+    x = np.ascontiguousarray(W_rot, np.float32).reshape(M, K // 256, 64, 4)
+    sq = x * x
+    p = ((sq[..., 0] + sq[..., 1]) + sq[..., 2]) + sq[..., 3]          # [M, nb, 64] fp32
+    lanes = np.arange(64)
+    for o in (32, 16, 8, 4, 2, 1):
+        p = p + p[..., lanes ^ o]
+    s = p[..., 0]
+    r = np.maximum(np.sqrt(s / np.float32(256)), np.float32(1e-10))
+    return (r * np.float32(scale)).astype(np.float32)
+
+
+def row_scale_ref(W_rot, cfg: dict):
+    """(rms [M, nb] fp32, d_row [M] fp32 (fp16 values), e [M, nb] int8, d [M, nb] fp32) as defined to the bit
+    for the quantizer (src/liqk_v2.py:938-946 with the float64 evaluation of log / mean / exp / log2):
+      d_row = max(fp16(fp32(exp(sum_b log(rms_b) / nb))), 1e-8)   (float64 log / exp, sum in block order)
+      e     = clamp(round_half_even(log2(fp32(rms / d_row)) / e_step), -2^(bits-1), 2^(bits-1) - 1)
+      d     = max(d_row * tab[e], 1e-8)                            (tab: the shared float32 exponent table)"""
+    W = W_rot.numpy() if hasattr(W_rot, "numpy") else np.asarray(W_rot)
+    rms = block_rms_ref(W, cfg.get("scale", 1.0))
+    M, nb = rms.shape
+    e_step, e_bits = float(cfg.get("e_step", 0.25)), int(cfg.get("e_bits", 5))
+    e_max = 1 << (e_bits - 1)
+    tab = _exp2_table(e_step, e_bits)
+    d_row = np.empty(M, np.float32)
+    e = np.empty((M, nb), np.int8)
+    for i in range(M):
+        ls = 0.0
+        for b in range(nb):
+            ls += math.log(float(rms[i, b]))
+        dr = np.float32(np.float16(np.float32(math.exp(ls / nb))))
+        d_row[i] = max(dr, np.float32(1e-8))
+        for b in range(nb):
+            ratio = np.float32(rms[i, b]) / d_row[i]
+            ev = round(math.log2(float(ratio)) / e_step)   # Python round: half to even
+            e[i, b] = min(max(ev, -e_max), e_max - 1)
+    d = np.maximum(d_row[:, None] * tab[e.astype(np.int64) + e_max], np.float32(1e-8)).astype(np.float32)
+    return rms, d_row, e, d
+
+
+def row_scale_torch_fp32(W_rot: torch.Tensor, cfg: dict):
+    """The reference's own formulation, verbatim in torch fp32 on the CPU (src/liqk_v2.py:941-946): used only to
+    count where the fp32 reductions and transcendental functions put d_row or e on the other side of a rounding
+    boundary than the exact definition above."""
     M, K = W_rot.shape
     nblocks = K // QK_K
     rms_rb = W_rot.float().view(M, nblocks, QK_K).square().mean(dim=2).sqrt().clamp(min=1e-10) * cfg.get("scale", 1.0)
@@ -27,6 +86,44 @@ def row_scale_ref(W_rot: torch.Tensor, cfg: dict):
     e_rb = torch.round(torch.log2(rms_rb / d_row.unsqueeze(1)) / e_step).clamp(-e_max, e_max - 1)
     d_rb_all = d_row.unsqueeze(1) * torch.exp2(e_step * e_rb)
     return rms_rb, d_row, e_rb, d_rb_all
+
+
+def suh_ref(W, H, seed: int = 1337, row_weights=None) -> np.ndarray:
+    """suh [K] float32 (fp16 values) of src/liqk_v2.py:409-441 evaluated in float64 (numpy): exact squares,
+    column means, the normalizations, col_rms^0.5 h_std^-0.25 clamped to [0.25, 4], times the Rademacher signs
+    (the reference's own torch CPU generator draw, src/iqk_format.py:173-179), rounded once to fp16."""
+    W = (W.float().numpy() if hasattr(W, "numpy") else np.asarray(W, np.float32)).astype(np.float64)
+    Hd = np.diag(H.double().numpy() if hasattr(H, "numpy") else np.asarray(H, np.float64)).astype(np.float64)
+    M, K = W.shape
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(seed)
+    signs = (torch.randint(0, 2, (K,), generator=gen, dtype=torch.int64) * 2 - 1).numpy().astype(np.float64)
+    sq = W * W
+    if row_weights is not None:
+        rw = np.asarray(row_weights, np.float64)
+        rw = np.maximum(rw, rw.mean() * 0.1)
+        rw = np.clip(rw / max(rw.mean(), 1e-12), 0.25, 4.0)
+        sq = sq * rw[:, None]
+    col_rms = np.maximum(np.sqrt(sq.sum(axis=0) / M), 1e-6)
+    col_rms = col_rms / max(col_rms.mean(), 1e-6)
+    h_std = np.sqrt(np.maximum(Hd, 1e-8))
+    h_std = h_std / max(h_std.mean(), 1e-6)
+    scale = np.clip(np.sqrt(col_rms) * np.power(h_std, -0.25), 0.25, 4.0)
+    return (signs * scale).astype(np.float16).astype(np.float32)
+
+
+def suh_torch_fp32(W: torch.Tensor, H: torch.Tensor, seed: int = 1337) -> torch.Tensor:
+    """The reference's fp32 torch text of the same scale (src/liqk_v2.py:419-434, no row weights), to count the
+    fp16 rounding-boundary flips of the fp32 evaluation against the float64 one."""
+    K = W.shape[1]
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(seed)
+    signs = (torch.randint(0, 2, (K,), generator=gen, dtype=torch.int64) * 2 - 1).float()
+    col_rms = W.float().square().mean(dim=0).sqrt().clamp(min=1e-6)
+    col_rms = col_rms / col_rms.mean().clamp(min=1e-6)
+    h_std = torch.diagonal(H.float()).clamp(min=1e-8).sqrt()
+    h_std = h_std / h_std.mean().clamp(min=1e-6)
+    return (signs * ((col_rms ** 0.5) * (h_std ** -0.25)).clamp(0.25, 4.0)).to(torch.float16).to(torch.float32)
 
 
 def factor_hessian_ref(H_rot: torch.Tensor, damp: float):
@@ -57,7 +154,8 @@ def quantize_rows_ref(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: torch.Te
     idx = torch.empty((M, K), dtype=torch.int16)
     gim = torch.empty((M, K), dtype=torch.uint8)
     if d_rb_all is None:
-        _, _, _, d_rb_all = row_scale_ref(W_rot, cfg)
+        _, _, _, d_np = row_scale_ref(W_rot, cfg)
+        d_rb_all = torch.from_numpy(d_np)
     first_x = None
     for ibl in range(nblocks):
         c0, c1 = ibl * QK_K, (ibl + 1) * QK_K

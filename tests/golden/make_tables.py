@@ -1,7 +1,7 @@
 """Extracts the TCQ format tables (trained LUTs, gain steps, masks, scales) from a reference checkout into
-tcq_tables.json. Data only: the numbers must be identical for .ltq compatibility.
+ltq-research_amd/ltq_amd/data/tcq_tables.json. Data only: the numbers must be identical for .ltq compatibility.
 
-    python ltq-research_amd/ltq_amd/data/make_tables.py /root/reference
+    python tests/golden/make_tables.py /root/reference
 
 Sources: src/liqk_v2.py:786-833 (TCQ_CONFIG literals, R / RH variants, TCQ_X_SCALE, read as text with ast)
 and results/tcq_x_tables.json (night-2 tail-biting tables)."""
@@ -33,7 +33,7 @@ def main(ref: str):
     out = {"base": base, "variants": variants, "x_scale": x_scale,
            "x_tables": {k: {kk: v[kk] for kk in ("K", "h", "step", "m_extra", "lut", "sub", "pp") if kk in v}
                         for k, v in x_tables.items()}}
-    dst = Path(__file__).resolve().parent / "tcq_tables.json"
+    dst = Path(__file__).resolve().parents[2] / "ltq-research_amd" / "ltq_amd" / "data" / "tcq_tables.json"
     dst.write_text(json.dumps(out, indent=1))
     print("wrote", dst, len(out["x_tables"]), "x tables,", len(variants), "variants")
 

@@ -112,6 +112,40 @@ def test_gpu_fwht_cols_matches_transposed_rows(oracle, cols, mode):
 
 
 @pytest.mark.gpu
+def test_suh_ref_pins():
+    """The oracle's suh: float64 definition (sign = Rademacher sign, |suh| the fp16 rounding of the clamped scale
+    computed in float64 by torch), the clamp at 0.25 / 4, row weights, and flips against the reference's fp32
+    text only on fp16 rounding boundaries (none expected at these sizes)."""
+    from oracle import liqk_ref
+    from ltq_amd.rotation import make_rademacher_signs
+    g = torch.Generator().manual_seed(9)
+    M, K = 96, 1024
+    W = torch.randn((M, K), generator=g) * 0.02
+    W[:, 5] *= 100      # clamps at 4
+    W[:, 6] *= 1e-4     # clamps at 0.25
+    X = torch.randn((300, K), generator=g)
+    H = X.T @ X / 300
+    s = liqk_ref.suh_ref(W, H, seed=1337)
+    signs = make_rademacher_signs(K, 1337, "cpu").numpy()
+    assert np.array_equal(np.sign(s), signs)
+    cr = W.double().square().mean(0).sqrt()
+    cr = cr / cr.mean()
+    hs = H.double().diagonal().sqrt()
+    hs = hs / hs.mean()
+    sc = (cr.sqrt() * hs.pow(-0.25)).clamp(0.25, 4.0)
+    assert np.array_equal(np.abs(s), sc.to(torch.float16).float().numpy())
+    assert abs(s[5]) == 4.0 and abs(s[6]) == 0.25
+    flips = int((torch.from_numpy(s) != liqk_ref.suh_torch_fp32(W, H)).sum())
+    print(f"suh: {flips} of {K} differ from the fp32 torch text")
+    assert flips <= K // 200
+    # row weights: uniform weights give the unweighted scale; a weighted row moves the column rms
+    assert np.array_equal(liqk_ref.suh_ref(W, H, row_weights=np.full(M, 3.0)), s)
+    rw = np.ones(M)
+    rw[0] = 100.0
+    assert not np.array_equal(liqk_ref.suh_ref(W, H, row_weights=rw), s)
+
+
+@pytest.mark.gpu
 def test_gpu_compute_optimal_suh(oracle):
     """suh and the rotated W / H of the reference recipe, with H rotated on both sides by the kernels."""
     from ltq_amd.rotation import compute_optimal_suh, make_rademacher_signs
@@ -122,16 +156,11 @@ def test_gpu_compute_optimal_suh(oracle):
     H = X.T @ X / 300
     W_rot, H_rot, suh = compute_optimal_suh(W.to(DEV), H.to(DEV), seed=1337)
     torch.cuda.synchronize()
-    # suh recomputed on the CPU (torch reductions: tolerance on the scale, exact signs and fp16 rounding grid)
-    signs = make_rademacher_signs(K, 1337, "cpu")
-    col_rms = W.float().square().mean(dim=0).sqrt().clamp(min=1e-6)
-    col_rms = col_rms / col_rms.mean()
-    h_std = H.diagonal().clamp(min=1e-8).sqrt()
-    h_std = h_std / h_std.mean()
-    suh_ref = (signs * ((col_rms ** 0.5) * (h_std ** -0.25)).clamp(0.25, 4.0)).half().float()
+    from oracle import liqk_ref
     suh_c = suh.cpu()
+    signs = make_rademacher_signs(K, 1337, "cpu")
     assert torch.equal(torch.sign(suh_c), signs)
-    assert (suh_c - suh_ref).abs().max() <= 2e-3 * suh_ref.abs().max()
+    assert np.array_equal(_u32(suh_c.numpy()), _u32(liqk_ref.suh_ref(W, H, seed=1337)))  # bit-exact
     # given the device's suh, the rotations are exact
     Wr = oracle.fwht256_ref((W.float() / suh_c).numpy())
     assert np.array_equal(_u32(W_rot.cpu().numpy()), _u32(Wr))
