@@ -27,6 +27,24 @@ int tcq_viterbi(const float* x, const float* w, const float* tab, const float* g
                 int G, int Gfull, int m, int sub, int U_hi, int mix, int m2, int m3, int m4, int nl, int ld, int rot,
                 uint32_t* pbits, int pp, void* stream);
 
+/* tcq_viterbi without any caller workspace, for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc). No counterpart in the reference: its C ABI
+ * takes bp / gsel / gcand / pbits from the caller. Same arguments, meaning and results as tcq_viterbi with those
+ * four dropped; the decision words and gain-candidate choices live in a static device array of
+ * tcq_viterbi_static_bytes() bytes (96 MiB) that every GPU running the library holds until the process ends
+ * (enough for 300 TCQ275X2 tiles of 256 steps). Returns -2, before touching any device, when a call needs more
+ * than that; -1 / HIP error codes as tcq_viterbi. The entry point allocates nothing. Calls on one GPU share its
+ * array: calls that overlap on one GPU (different streams or host threads) race; calls in one stream do not.
+ * Nothing in the array needs clearing between calls (every word is written before it is read). */
+int tcq_viterbi_static(const float* x, const float* w, const float* tab, const float* gains, float* rec,
+                       const int* init_st, int* end_st, const float* tab_hi, const float* gains_hi, int* best,
+                       int* code, int* mid_st, int mid_t, int tail, int N, int T, int S, int U, int G, int Gfull,
+                       int m, int sub, int U_hi, int mix, int m2, int m3, int m4, int nl, int ld, int rot, int pp,
+                       void* stream);
+
+/* Size in bytes of tcq_viterbi_static's per-device scratch array. Host-only. */
+long tcq_viterbi_static_bytes(void);
+
 /* LUT sub-block quantization of the diagonal profile: for S sub-blocks of 16 weights xs[S, 16] with weights
  * dh[S, 16], bucket b = clamp(rint(x * inv_step + half_b), 0, nb - 1) picks a row of 64 candidates of lut[nb, 64];
  * the first candidate with the lowest sum_j dh (xs - lut[b_j][c])^2 gives out[S, 16] = lut[b_j][c]. Same

@@ -67,6 +67,7 @@ struct TcqArgs {
     uint32_t* pbits;       // scratch (reference size [N, T/2, G, S/32] for pp=1, [N, T/4, G, 9, S/32] for pp>=2)
     int pp;
     int scratch_T = 0;     // > 0: the step count bp / pbits / gcand are sized for per tile (fused pass 1), else T
+    long tile_words = 0;   // > 0: compact scratch, tile n's decision words at bp + n * tile_words (pbits unused)
 };
 
 LTQ_DEV int parity32(uint32_t v) { return __builtin_popcount(v) & 1; }
@@ -586,9 +587,12 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
             ok[b][j] = s0 < 0 || (sm1 >> 1) == (s0 & (HALF - 1));
         }
 
-    const DecMap dm{a.bp + (size_t)n * Ts * G * (S / 32),
-                    a.pbits ? a.pbits + (size_t)n * (scratch_words(Ts, G, S, a.pp) - (long)Ts * G * (S / 32)) : nullptr,
-                    (long)Ts * G * (S / 32)};
+    const DecMap dm = a.tile_words > 0
+                          ? DecMap{a.bp + (size_t)n * a.tile_words, nullptr, a.tile_words}
+                          : DecMap{a.bp + (size_t)n * Ts * G * (S / 32),
+                                   a.pbits ? a.pbits + (size_t)n * (scratch_words(Ts, G, S, a.pp) - (long)Ts * G * (S / 32))
+                                           : nullptr,
+                                   (long)Ts * G * (S / 32)};
     const int nph = T / 2;
     const int nchunk = (nph + NPC - 1) / NPC;
     const long chunk_words = (long)G * Q * 64 * NW;
@@ -1331,8 +1335,28 @@ inline int tcq_check(const TcqArgs& a)
         nl * U_hi > 4 * kMaxU)
         return -1;
     if ((S != 1024 && S != 256) || (G != 1 && G != 2 && G != 3 && G != 4 && G != 8)) return -1;
-    if (T <= 0 || !a.bp || (pp && !a.pbits) || !a.best || !a.rec) return -1;
+    if (T <= 0 || !a.bp || (pp && !a.pbits && a.tile_words <= 0) || !a.best || !a.rec) return -1;
     return 0;
+}
+
+// decision words one tile of this configuration needs (the instance tcq_dispatch selects), -1 if none serves it
+inline long tcq_needed_words(const TcqArgs& a)
+{
+    if (a.S == 256) return needed_words<8, 2, 0>(a.T, a.G);
+    const bool r3 = a.G > 4;
+    switch (a.pp) {
+        case 0: return r3 ? needed_words<10, 3, 0>(a.T, a.G) : needed_words<10, 2, 0>(a.T, a.G);
+        case 1: return r3 ? needed_words<10, 3, 1>(a.T, a.G) : needed_words<10, 2, 1>(a.T, a.G);
+        case 2: return r3 ? needed_words<10, 3, 2>(a.T, a.G) : needed_words<10, 2, 2>(a.T, a.G);
+        case 3: return r3 ? needed_words<10, 3, 3>(a.T, a.G) : needed_words<10, 2, 3>(a.T, a.G);
+        default: return -1;
+    }
+}
+
+// decision words available per tile: the compact window, or bp + pbits in the reference's shapes
+inline long tcq_capacity_words(const TcqArgs& a)
+{
+    return a.tile_words > 0 ? a.tile_words : scratch_words(a.scratch_T > 0 ? a.scratch_T : a.T, a.G, a.S, a.pp);
 }
 
 // Calls f.template run<NU, RB, MD, NL>() for the instance serving a (RB = 3 when G = 8 at S = 1024, so that a
@@ -1342,8 +1366,7 @@ int tcq_dispatch(const TcqArgs& a, const F& f)
 {
     auto go = [&](auto nu, auto rb, auto md) -> int {
         constexpr int NU = decltype(nu)::value, RB = decltype(rb)::value, MD = decltype(md)::value;
-        if (needed_words<NU, RB, MD>(a.T, a.G) > scratch_words(a.scratch_T > 0 ? a.scratch_T : a.T, a.G, a.S, a.pp))
-            return -1;
+        if (needed_words<NU, RB, MD>(a.T, a.G) > tcq_capacity_words(a)) return -1;
         switch (a.nl) {
             case 4: return f.template run<NU, RB, MD, 4>();
             case 8: return f.template run<NU, RB, MD, 8>();
@@ -1356,8 +1379,7 @@ int tcq_dispatch(const TcqArgs& a, const F& f)
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
     if (a.S == 256) {
-        if (needed_words<8, 2, 0>(a.T, a.G) > scratch_words(a.scratch_T > 0 ? a.scratch_T : a.T, a.G, a.S, a.pp))
-            return -1;
+        if (needed_words<8, 2, 0>(a.T, a.G) > tcq_capacity_words(a)) return -1;
         return f.template run<8, 2, 0, 4>();
     }
     const bool r3 = a.G > 4;

@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "tcq_launch.h"
 
 #include "ltq_hip.h"
@@ -125,6 +127,72 @@ extern "C" int tcq_viterbi_tb(const float* x, const float* w, const float* tab, 
     int rc = tcq_dispatch(a1, GpuLaunchTbCheck{});
     if (rc != 0) return rc;
     rc = tcq_dispatch(a2, GpuLaunchTb{a1, a2, (hipStream_t)stream});
+    if (rc != 0) return rc;
+    return (int)hipGetLastError();
+}
+
+// ---- the allocation-free entry point ---------------------------------------------------------------------
+// Decision scratch in a file-scope device array. Each GPU that loads the library holds its own copy until the
+// process ends; host code reaches a device's copy only through the address hipGetSymbolAddress returns while
+// that device is current (the array's name is a host-side stand-in), kept per device.
+namespace {
+
+constexpr size_t kStaticScratchBytes = size_t(96) << 20;
+static __device__ __align__(256) uint32_t scratch[kStaticScratchBytes / 4];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};
+
+// this device's copy of the array, looked up once per device
+int static_scratch(void** out)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= 64) return -1;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!ptr) return -1;
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
+}  // namespace
+
+extern "C" long tcq_viterbi_static_bytes(void) { return (long)kStaticScratchBytes; }
+
+extern "C" int tcq_viterbi_static(const float* x, const float* w, const float* tab, const float* gains, float* rec,
+                                  const int* init_st, int* end_st, const float* tab_hi, const float* gains_hi, int* best,
+                                  int* code, int* mid_st, int mid_t, int tail, int N, int T, int S, int U, int G,
+                                  int Gfull, int m, int sub, int U_hi, int mix, int m2, int m3, int m4, int nl, int ld,
+                                  int rot, int pp, void* stream)
+{
+    using namespace ltq;
+    // validation runs on stand-in scratch pointers (tcq_check only tests them for null; they are replaced before
+    // the launch): the sizes come first, so an oversized call is refused before any device is touched
+    uint32_t* const probe = reinterpret_cast<uint32_t*>(uintptr_t(256));
+    const bool cand = G < Gfull;
+    TcqArgs a{x, w, tab, gains, rec, probe, nullptr, init_st, end_st, tab_hi, gains_hi,
+              cand ? reinterpret_cast<uint8_t*>(probe) : nullptr, best, code, mid_st, mid_t, tail, N, T, S, U, G,
+              Gfull, m, sub, U_hi, mix, m2, m3, m4, nl, ld, rot, nullptr, pp};
+    if (N <= 0 || T <= 0 || G <= 0 || sub <= 0) return -1;
+    const long need = tcq_needed_words(a);
+    if (need <= 0) return -1;
+    a.tile_words = (need + 63) / 64 * 64;  // 256-byte aligned tile windows
+    const size_t dec_bytes = (size_t)N * (size_t)a.tile_words * 4;
+    const size_t cand_bytes = cand ? ((size_t)N * (T / sub) * G + 255) / 256 * 256 : 0;
+    if (dec_bytes + cand_bytes > kStaticScratchBytes) return -2;
+    if (tcq_check(a) != 0 || (getenv("TCQ_BLOCK") && nl != 4)) return -1;
+    void* base = nullptr;
+    if (const int rc = static_scratch(&base)) return rc;
+    a.bp = static_cast<uint32_t*>(base);
+    a.gcand = cand ? static_cast<uint8_t*>(base) + dec_bytes : nullptr;
+    const int rc = tcq_dispatch(a, GpuLaunch{a, (hipStream_t)stream});
     if (rc != 0) return rc;
     return (int)hipGetLastError();
 }

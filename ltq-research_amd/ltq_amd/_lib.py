@@ -19,6 +19,9 @@ SIGNATURES = {
     "tcq_viterbi": (ci, [vp] * 15 + [ci] * 18 + [vp, ci, vp]),
     # both tail-biting passes in one launch (no reference counterpart; the two calls of src/tcq_proto.py:584-609)
     "tcq_viterbi_tb": (ci, [vp] * 14 + [ci] * 17 + [vp, ci, ci, ci, ci, vp]),
+    # tcq_viterbi without caller workspace (no reference counterpart): 12 pointers, 19 ints, stream
+    "tcq_viterbi_static": (ci, [vp] * 12 + [ci] * 19 + [vp]),
+    "tcq_viterbi_static_bytes": (cl, []),
     # src/cuda/tcq_viterbi.cu:806-807; src/tcq_proto.py:531-532
     "lut_subs_quant": (ci, [vp] * 4 + [ci, cf, cf, ci, vp]),
     # FWHT-256 (src/iqk_format.py:153-170), rows with a fused scale / columns

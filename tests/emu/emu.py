@@ -33,6 +33,10 @@ def lib(asan: bool = False):
         L = ctypes.CDLL(str(so))
         L.tcq_viterbi_emu.restype = ctypes.c_int
         L.tcq_viterbi_emu.argtypes = [ctypes.c_void_p] * 15 + [ctypes.c_int] * 18 + [ctypes.c_void_p, ctypes.c_int]
+        L.tcq_needed_words_emu.restype = ctypes.c_long
+        L.tcq_needed_words_emu.argtypes = [ctypes.c_int] * 4
+        L.tcq_viterbi_compact_emu.restype = ctypes.c_int
+        L.tcq_viterbi_compact_emu.argtypes = [ctypes.c_void_p] * 12 + [ctypes.c_int] * 16 + [ctypes.c_long]
         L.tcq_viterbi_tb_emu.restype = ctypes.c_int
         L.tcq_viterbi_tb_emu.argtypes = [ctypes.c_void_p] * 14 + [ctypes.c_int] * 17 + [ctypes.c_void_p] + [ctypes.c_int] * 4
         _LIB[asan] = L
@@ -119,3 +123,40 @@ def tcq_viterbi_tb(x, w, tab, gains, *, n_cand=0, S=1024, U=None, m=359, sub=16,
     if rc != 0:
         raise RuntimeError(f"tcq_viterbi_tb_emu: error code {rc}")
     return {"rec": rec, "code": code, "best": best}
+
+
+def tcq_viterbi_compact(x, w, tab, gains, *, init_st=None, n_cand=0, mid_t=0, tail=False, S=1024, m=359, sub=16,
+                        m_extra=(), steps=0, rot=0, pp=0, guard=4096, asan=False):
+    """The kernel body with the compact decision-scratch window of tcq_viterbi_static: tile_words = the words a
+    tile needs rounded up to 64, the buffer exactly N * tile_words words plus `guard` sentinel words after it.
+    Returns (the tcq_viterbi-style result dict, whether every guard word is untouched)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    N, ld = x.shape
+    T = steps or ld
+    nl = 4 << len(m_extra)
+    tab = np.ascontiguousarray(tab, np.float32)
+    gains = np.ascontiguousarray(gains, np.float32)
+    U = tab.size // nl
+    Gfull = gains.size
+    G = n_cand if 0 < n_cand < Gfull else Gfull
+    L = lib(asan)
+    need = L.tcq_needed_words_emu(T, S, G, pp)
+    assert need > 0
+    tw = (need + 63) // 64 * 64
+    bp = np.full(N * tw + guard, 0xDEADBEEF, np.uint32)
+    rec = np.zeros((N, ld), np.float32)
+    code = np.zeros((N, ld), np.int32)
+    best = np.zeros(N, np.int32)
+    end = np.zeros(N, np.int32)
+    mid = np.zeros(N, np.int32) if mid_t else None
+    gcand = np.zeros((N, T // sub, G), np.uint8) if G < Gfull else None
+    init = np.ascontiguousarray(np.asarray(init_st, dtype=np.int32)) if init_st is not None else None
+    me = (list(m_extra) + [0, 0])[:2]
+    rc = L.tcq_viterbi_compact_emu(_p(x), _p(w), _p(tab), _p(gains), _p(rec), _p(bp), _p(init), _p(end), _p(gcand),
+                                   _p(best), _p(code), _p(mid), mid_t, int(tail), N, T, S, U, G, Gfull, m, sub, nl,
+                                   me[0], me[1], ld, rot, int(pp), tw)
+    if rc != 0:
+        raise RuntimeError(f"emulated compact tcq_viterbi: error code {rc}")
+    guard_ok = bool(np.all(bp[N * tw:] == 0xDEADBEEF))
+    return {"rec": rec, "code": code, "best": best, "end": end, "mid": mid}, guard_ok

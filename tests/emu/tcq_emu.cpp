@@ -206,3 +206,28 @@ extern "C" int tcq_viterbi_emu(const float* x, const float* w, const float* tab,
     if (N <= 0) return N == 0 ? 0 : -1;
     return tcq_dispatch(a, CpuRun{a});
 }
+
+// the compact scratch window of the allocation-free entry point: tile n's decision words at bp + n * tile_words
+extern "C" long tcq_needed_words_emu(int T, int S, int G, int pp)
+{
+    TcqArgs a{};
+    a.T = T;
+    a.S = S;
+    a.G = G;
+    a.pp = pp;
+    return tcq_needed_words(a);
+}
+
+extern "C" int tcq_viterbi_compact_emu(const float* x, const float* w, const float* tab, const float* gains, float* rec,
+                                       uint32_t* bp, const int* init_st, int* end_st, uint8_t* gcand, int* best,
+                                       int* code, int* mid_st, int mid_t, int tail, int N, int T, int S, int U, int G,
+                                       int Gfull, int m, int sub, int nl, int m2, int m3, int ld, int rot, int pp,
+                                       long tile_words)
+{
+    TcqArgs a{x, w, tab, gains, rec, bp, nullptr, init_st, end_st, tab, gains, gcand, best, code, mid_st,
+              mid_t, tail, N, T, S, U, G, Gfull, m, sub, U, 0, m2, m3, 0, nl, ld, rot, nullptr, pp};
+    a.tile_words = tile_words;
+    if (tile_words <= 0 || tcq_check(a) != 0) return -1;
+    if (N <= 0) return N == 0 ? 0 : -1;
+    return tcq_dispatch(a, CpuRun{a});
+}

@@ -73,3 +73,24 @@ def test_hessian_entry_points_reject_bad_arguments_without_a_device():
     assert fin(buf, 0, 8, 1.0, buf, 8, None) == -1
     assert fin(buf, 8, 7, 1.0, buf, 8, None) == -1
     assert fin(None, 8, 8, 1.0, buf, 8, None) == -1
+
+
+def test_static_entry_refuses_oversized_calls_before_device_work():
+    """tcq_viterbi_static checks its scratch need against the static array first: an oversized call returns -2
+    without touching a device (this machine has none), and an invalid one -1."""
+    from ltq_amd import _lib
+    so = ROOT / "ltq-research_amd" / "ltq_amd" / "libltq_hip.so"
+    if not so.exists():
+        pytest.skip("libltq_hip.so not built (run __graft_entry__.build())")
+    L = _lib.lib()
+    cap = L.tcq_viterbi_static_bytes()
+    assert cap == 96 << 20
+    fake = 4096  # stand-in addresses: the call must return before using them
+    # TCQ275X2's closing pass needs 320 KiB per tile: 1000 tiles do not fit
+    args = [fake] * 5 + [None, None, fake, fake, fake, fake, None]
+    ints = [0, 1, 1000, 256, 1024, 4, 4, 4, 359, 16, 4, 0, 241, 0, 0, 8, 256, 128]
+    assert L.tcq_viterbi_static(*args, *ints, 2, None) == -2
+    ints[2] = 300  # 300 tiles fit; but T not a multiple of sub is invalid -> -1 (still before any device call)
+    ints[3] = 250
+    ints[16] = 256
+    assert L.tcq_viterbi_static(*args, *ints, 2, None) == -1

@@ -110,3 +110,39 @@ def test_emulated_fused_tail_biting_matches_two_pass_driver(ci):
                                           m_extra=c["ext"], pair_parity=c["pp"], return_code=True)
     assert np.array_equal(e["rec"].view(np.uint32), np.asarray(rec, np.float32).view(np.uint32))
     assert np.array_equal(e["code"], (np.asarray(gi, np.int64) << 16 | np.asarray(ix, np.int64)).astype(np.int32))
+
+
+COMPACT_CASES = [
+    dict(pp=2, ext=(241,), G=4, T=256, N=3),                         # TCQ275X2 closing pass: whole chunks
+    dict(pp=2, ext=(241,), G=4, T=64, N=3, ld=256, rot=96, mid_t=32),  # its first pass (window 32)
+    dict(pp=0, ext=(241,), G=4, Gfull=8, n_cand=4, T=64, N=2),        # candidates: gcand beside the words
+    dict(pp=1, ext=(241,), G=2, T=40, N=2, sub=8),                   # partial last chunk (general walker)
+    dict(pp=0, ext=(), G=8, T=48, N=2),                              # G = 8
+]
+
+
+@pytest.mark.parametrize("ci", range(len(COMPACT_CASES)))
+def test_emulated_compact_scratch_window(oracle, ci):
+    """The decision-scratch layout of tcq_viterbi_static (each tile's words in a window of its needed words
+    rounded up to 64, nothing else) gives the oracle's results and writes nothing past the last window."""
+    import emu
+    c = COMPACT_CASES[ci]
+    rng = np.random.default_rng(300 + ci)
+    nl = 4 << len(c["ext"])
+    U, Gf, N = 4, c.get("Gfull", c["G"]), c["N"]
+    ld = c.get("ld", c["T"])
+    tab = rng.standard_normal(nl * U).astype(np.float32)
+    gains = (2.0 ** ((np.arange(Gf) - (Gf - 1) / 2) * 0.22)).astype(np.float32)
+    x = (rng.standard_normal((N, ld)) * 1.2).astype(np.float32)
+    w = (rng.random((N, ld)) + 0.5).astype(np.float32)
+    kw = dict(sub=c.get("sub", 16), m_extra=c["ext"], pp=c["pp"], n_cand=c.get("n_cand", 0),
+              steps=c["T"] if ld != c["T"] else 0, rot=c.get("rot", 0), mid_t=c.get("mid_t", 0))
+    o = oracle.tcq_viterbi(x, w, tab, gains, want_end=True, **kw)
+    e, guard_ok = emu.tcq_viterbi_compact(x, w, tab, gains, **kw)
+    assert guard_ok
+    assert np.array_equal(o["best"], e["best"])
+    if kw["mid_t"]:
+        assert np.array_equal(o["mid"], e["mid"])
+    else:
+        assert np.array_equal(o["code"], e["code"])
+        assert np.array_equal(o["rec"].view(np.uint32), e["rec"].view(np.uint32))
