@@ -22,7 +22,8 @@
 //     x_next           = w[:, s1:s1+16] * (1 / d)             (next sub-block's Viterbi tiles, t = 16 r + c)
 //     idx[:, s0:s1]    = code & 0xFFFF, gi[:, s0:s1] = code >> 16   (optional: the PACK fields, src/liqk_v2.py:919-921)
 // with the element-wise products and the division rounded as the reference's torch code rounds them; the two
-// small contractions accumulate with FMAs (a library GEMM orders its sums differently as well).
+// small contractions are fma chains over k = 0..15 in ascending order from 0 (then w - acc), and the value each
+// element had when its Viterbi ran is optionally recorded (fed).
 // One workgroup per tile; roofline: L2 (the block's working copy and U rows are re-read per sub-block).
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
@@ -77,7 +78,8 @@ __global__ __launch_bounds__(256) void ldlq_sub_kernel(float* __restrict__ wk, l
                                                        float* __restrict__ G, long ldg,
                                                        float* __restrict__ xnext, long M,
                                                        const int* __restrict__ code, int16_t* __restrict__ idx,
-                                                       long ld_idx, uint8_t* __restrict__ gi, long ld_gi)
+                                                       long ld_idx, uint8_t* __restrict__ gi, long ld_gi,
+                                                       float* __restrict__ fed, long ld_fed)
 {
     __shared__ float s_err[16][17];
     __shared__ float s_d[16];
@@ -94,10 +96,12 @@ __global__ __launch_bounds__(256) void ldlq_sub_kernel(float* __restrict__ wk, l
         idx[row * ld_idx + s0 + c] = (int16_t)(cv & 0xFFFF);
         gi[row * ld_gi + s0 + c] = (uint8_t)(cv >> 16);
     }
+    const float wv = wk[row * ldw + s0 + c];  // the value this sub-block's Viterbi saw (times 1 / d)
+    if (fed) fed[row * ld_fed + s0 + c] = wv;
     __syncthreads();
     const float dr = s_d[r];
-    // residual of this element, then err[r][c] = sum_k resid[r][k] * uinv[s0+k][s0+c]
-    const float resid = wk[row * ldw + s0 + c] - dr * g;
+    // residual of this element, then err[r][c] = sum_k resid[r][k] * uinv[s0+k][s0+c] (fma chain, k ascending)
+    const float resid = wv - dr * g;
     s_err[r][c] = resid;
     __syncthreads();
     float e = 0.f;
@@ -158,13 +162,15 @@ extern "C" int ltq_ldlq_prep(const float* wk, long ldw, const float* d, long ldd
 
 extern "C" int ltq_ldlq_sub(float* wk, long ldw, const float* rec, const float* d, long ldd, const float* uinv,
                             long ldi, const float* ublk, long ldu, int ib, float* G, long ldg, float* xnext, long M,
-                            const int* code, int16_t* idx, long ld_idx, uint8_t* gi, long ld_gi, void* stream)
+                            const int* code, int16_t* idx, long ld_idx, uint8_t* gi, long ld_gi, float* fed,
+                            long ld_fed, void* stream)
 {
     if (M < 0 || M % 16 || ib < 0 || ib > 15 || ldw < 256 || ldi < 256 || ldu < 256 || ldg < 256 || ldd < 1) return -1;
     if (code && (!idx || !gi || ld_idx < 256 || ld_gi < 256)) return -1;
+    if (fed && ld_fed < 256) return -1;
     if (M == 0) return 0;
     if (!wk || !rec || !d || !uinv || !ublk || !G) return -1;
     hipLaunchKernelGGL(ldlq_sub_kernel, dim3((unsigned)(M / 16)), dim3(256), 0, (hipStream_t)stream, wk, ldw, rec, d, ldd,
-                       uinv, ldi, ublk, ldu, 16 * ib, G, ldg, xnext, M, code, idx, ld_idx, gi, ld_gi);
+                       uinv, ldi, ublk, ldu, 16 * ib, G, ldg, xnext, M, code, idx, ld_idx, gi, ld_gi, fed, ld_fed);
     return (int)hipGetLastError();
 }

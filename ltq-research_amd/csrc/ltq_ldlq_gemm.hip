@@ -1,0 +1,262 @@
+// The two dense contractions of the LDLQ block error feedback on the matrix cores (gfx950 fp32 MFMA).
+//
+// After the 16 sub-blocks of a 256-column block [c0, c1) (src/liqk_v2.py:972-979):
+//   ltq_ldlq_err:     E = (W_start - d * G) @ U_blk_inv          [M, 256] @ [256, 256], stored transposed (E^T)
+//                     (and W_hat[:, c0:c1] = d * G, the block's reconstruction)
+//   ltq_ldlq_update:  W[:, c1:] -= E @ U[c0:c1, c1:]             [M, 256] @ [256, K - c1]
+//                     (and the next block's working copy and first Viterbi tiles from the updated columns)
+// with the element-wise products and differences rounded as the reference's torch code rounds them.
+//
+// Summation order. Every output is the fp32 fused multiply-add chain over k = 0, 1, ..., 255 in ascending order
+// starting from 0, i.e. acc = fma(a[k], b[k], acc), then (update) w - acc. v_mfma_f32_16x16x4_f32 computes
+// exactly that chain over its four k (measured on gfx950: every output of random and cancelling inputs equals
+// the ascending correctly rounded FMA chain, no other ordering or single rounding does), and the kernels issue
+// the instructions of an output in ascending k, so the result is a defined function of the inputs that a CPU
+// restatement with fmaf reproduces bit for bit. (A library GEMM's split-k and blocking orders are not fixed.)
+//
+// Tiling. A workgroup of 4 wavefronts computes a 128 x 128 output tile; wavefront (wr, wc) a 64 x 64 quarter
+// as 4 x 4 MFMA blocks of 16 x 16. k advances in stages of 16: the stage's A (128 x 16) and B (16 x 128)
+// operands go global -> registers -> LDS (k-major, row pitch 144 floats: each half-wavefront's operand reads
+// hit 32 distinct banks), double-buffered, one barrier per stage, the next stage's loads in flight during the
+// current stage's 64 MFMAs per wavefront. Workgroups are dealt to the 8 XCDs in contiguous tile ranges with
+// the row tile fastest, so the workgroups on one XCD share the U column panels in its L2.
+// Roofline: MFMA fp32 (157.3 TFLOP/s dense), 2 M 256 N flops per update.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ltq_hip.h"
+
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int BM = 128, BN = 128, KC = 16, LDP = 144, KD = 256;
+
+struct GemmArgs {
+    // A operand: AMODE 0 -> at[k * ld_a + i] (k-major E^T); AMODE 1 -> ws[i * ld_a + k] - d[i * ldd] * g[i * ldg + k]
+    const float* a;
+    long ld_a;
+    const float* g;
+    long ldg;
+    const float* d;
+    long ldd;
+    const float* b;  // B operand b[k * ldb + j], k < 256
+    long ldb;
+    long M, N;       // output rows, columns (N % 128 == 0)
+    // EPI 0: out[j * ld_out + i] = acc (transposed), what[i * ld_what + j] = d g (column tile 0's A values)
+    // EPI 1: out[i * ld_out + j] -= acc; wsub[i * ld_wsub + j] = new value for j < 256; xnext for j < 16
+    float* out;
+    long ld_out;
+    float* what;
+    long ld_what;
+    float* wsub;
+    long ld_wsub;
+    float* xnext;
+    const float* dnext;
+    long ld_dnext;
+    int tiles_m, tiles_n;
+};
+
+// XCD-aware tile order: block b runs on XCD b % 8; XCD x takes a contiguous range of tiles, row tile fastest
+__device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn)
+{
+    const int nt = tiles_m * tiles_n, q = nt / 8, r = nt % 8;
+    const int xcd = b % 8, slot = b / 8;
+    const int t = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
+    tm = t % tiles_m;
+    tn = t / tiles_m;
+}
+
+template <int AMODE, int EPI>
+__global__ __launch_bounds__(256) void ldlq_gemm_kernel(GemmArgs p)
+{
+    __shared__ __align__(16) float sA[2][KC][LDP];
+    __shared__ __align__(16) float sB[2][KC][LDP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave >> 1, wc = wave & 1;
+    int tm, tn;
+    tile_of((int)blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const long row0 = (long)tm * BM, col0 = (long)tn * BN;
+    const bool write_what = EPI == 0 && p.what != nullptr && tn == 0;
+
+    // staging registers of one stage: 2 float4 of A and 2 of B per thread
+    v4f ra[2], rb[2];
+    auto load_stage = [&](int k0) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int e = tid + 256 * q;
+            // B: row k = e / 32, columns 4 (e % 32) .. + 3
+            const int kb = e >> 5, jb = (e & 31) * 4;
+            rb[q] = *(const v4f*)(p.b + (long)(k0 + kb) * p.ldb + col0 + jb);
+            if constexpr (AMODE == 0) {
+                // A^T: row k = e / 32, output rows 4 (e % 32) .. + 3
+                const long i = row0 + (e & 31) * 4;
+                ra[q] = i < p.M ? *(const v4f*)(p.a + (long)(k0 + kb) * p.ld_a + i) : v4f{0.f, 0.f, 0.f, 0.f};
+            } else {
+                // A: output row r = e / 4, k = 4 (e % 4) .. + 3, computed as ws - d * g
+                const long i = row0 + (e >> 2);
+                const int k = k0 + (e & 3) * 4;
+                if (i < p.M) {
+                    const v4f w = *(const v4f*)(p.a + i * p.ld_a + k);
+                    const v4f gg = *(const v4f*)(p.g + i * p.ldg + k);
+                    const float dd = p.d[i * p.ldd];
+                    const v4f dg = v4f{dd * gg.x, dd * gg.y, dd * gg.z, dd * gg.w};
+                    if (write_what) *(v4f*)(p.what + i * p.ld_what + k) = dg;
+                    ra[q] = w - dg;
+                } else {
+                    ra[q] = v4f{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+        }
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int e = tid + 256 * q;
+            const int kb = e >> 5, jb = (e & 31) * 4;
+            *(v4f*)&sB[buf][kb][jb] = rb[q];
+            if constexpr (AMODE == 0) {
+                *(v4f*)&sA[buf][kb][(e & 31) * 4] = ra[q];
+            } else {
+                const int r = e >> 2, k = (e & 3) * 4;
+                sA[buf][k + 0][r] = ra[q].x;
+                sA[buf][k + 1][r] = ra[q].y;
+                sA[buf][k + 2][r] = ra[q].z;
+                sA[buf][k + 3][r] = ra[q].w;
+            }
+        }
+    };
+
+    v4f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+    constexpr int NST = KD / KC;
+    const int kl = lane >> 4, il = lane & 15;
+    for (int s = 0; s < NST; s++) {
+        const int buf = s & 1;
+        if (s + 1 < NST) load_stage((s + 1) * KC);
+#pragma unroll
+        for (int kk = 0; kk < KC; kk += 4) {
+            float av[4], bv[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) av[r] = sA[buf][kk + kl][wr * 64 + r * 16 + il];
+#pragma unroll
+            for (int c = 0; c < 4; c++) bv[c] = sB[buf][kk + kl][wc * 64 + c * 16 + il];
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[r], bv[c], acc[r][c], 0, 0, 0);
+        }
+        if (s + 1 < NST) {
+            store_stage(buf ^ 1);
+            __syncthreads();
+        }
+    }
+
+    // epilogue: block (r, c) register v is output row 16 r + 4 (lane / 16) + v, column 16 c + lane % 16
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const long i = row0 + wr * 64 + r * 16 + 4 * kl + v;
+            if (i >= p.M) continue;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const long j = col0 + wc * 64 + c * 16 + il;
+                if constexpr (EPI == 0) {
+                    p.out[j * p.ld_out + i] = acc[r][c][v];
+                } else {
+                    float* const o = p.out + i * p.ld_out + j;
+                    const float nv = *o - acc[r][c][v];
+                    *o = nv;
+                    if (p.wsub && j < KD) p.wsub[i * p.ld_wsub + j] = nv;
+                    if (p.xnext && j < 16) {
+                        const float inv = 1.0f / p.dnext[i * p.ld_dnext];
+                        p.xnext[(i >> 4) * 256 + (i & 15) * 16 + j] = nv * inv;
+                    }
+                }
+            }
+        }
+}
+
+int launch_gemm(int amode, int epi, GemmArgs p, hipStream_t st)
+{
+    p.tiles_m = (int)((p.M + BM - 1) / BM);
+    p.tiles_n = (int)(p.N / BN);
+    const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
+    if (grid == 0) return 0;
+    if (amode == 0 && epi == 1)
+        hipLaunchKernelGGL((ldlq_gemm_kernel<0, 1>), dim3(grid), dim3(256), 0, st, p);
+    else if (amode == 1 && epi == 0)
+        hipLaunchKernelGGL((ldlq_gemm_kernel<1, 0>), dim3(grid), dim3(256), 0, st, p);
+    else
+        return -1;
+    return (int)hipGetLastError();
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+extern "C" int ltq_ldlq_err(const float* wstart, long ldw, const float* G, long ldg, const float* d, long ldd,
+                            const float* uinv, long ldi, float* et, long ld_et, float* what, long ld_what, long M,
+                            void* stream)
+{
+    if (M < 0 || M % 16 || ldw < 256 || ldg < 256 || ldd < 1 || ldi < 256 || ld_et < M || (what && ld_what < 256))
+        return -1;
+    if (M == 0) return 0;
+    if (!wstart || !G || !d || !uinv || !et) return -1;
+    if ((ldw | ldg | ldi | ld_et | (what ? ld_what : 0)) & 3) return -1;
+    if (!aligned16(wstart) || !aligned16(G) || !aligned16(uinv) || !aligned16(et) || (what && !aligned16(what)))
+        return -1;
+    GemmArgs p{};
+    p.a = wstart;
+    p.ld_a = ldw;
+    p.g = G;
+    p.ldg = ldg;
+    p.d = d;
+    p.ldd = ldd;
+    p.b = uinv;
+    p.ldb = ldi;
+    p.M = M;
+    p.N = KD;
+    p.out = et;
+    p.ld_out = ld_et;
+    p.what = what;
+    p.ld_what = ld_what;
+    return launch_gemm(1, 0, p, (hipStream_t)stream);
+}
+
+extern "C" int ltq_ldlq_update(float* w, long ldw, const float* et, long ld_et, const float* u, long ldu, long M, long N,
+                               float* wsub, long ld_wsub, float* xnext, const float* dnext, long ld_dnext, void* stream)
+{
+    if (M < 0 || N < 0 || M % 16 || N % BN || ldw < N || ld_et < M || ldu < N || (wsub && (ld_wsub < KD || N < KD)) ||
+        (xnext && (!dnext || ld_dnext < 1 || N < 16)))
+        return -1;
+    if (M == 0 || N == 0) return 0;
+    if (!w || !et || !u) return -1;
+    if ((ld_et | ldu) & 3) return -1;
+    if (!aligned16(et) || !aligned16(u)) return -1;
+    GemmArgs p{};
+    p.a = et;
+    p.ld_a = ld_et;
+    p.b = u;
+    p.ldb = ldu;
+    p.M = M;
+    p.N = N;
+    p.out = w;
+    p.ld_out = ldw;
+    p.wsub = wsub;
+    p.ld_wsub = ld_wsub;
+    p.xnext = xnext;
+    p.dnext = dnext;
+    p.ld_dnext = ld_dnext;
+    return launch_gemm(0, 1, p, (hipStream_t)stream);
+}

@@ -6,12 +6,14 @@ Mirrors (same names, argument meaning, results and the module-level PACK switch)
   factor_hessian              src/liqk_v2.py:1066-1088 (damping, Cholesky of the flipped H, U, diag_w, U_blks_inv)
   row_scale                   src/liqk_v2.py:938-946  (HIP kernel ltq_row_scale)
   _quantize_rows_tcq_ldlq     src/liqk_v2.py:877-1021 (the row-scale branch: every tail-biting / R format;
-                                                       HIP kernels ltq_ldlq_prep / ltq_ldlq_sub per sub-block,
-                                                       tcq_viterbi two-pass tail-biting, library GEMM across blocks)
-  quantize_matrix_liqk_v2     src/liqk_v2.py:1029-1200 (single TCQ spec or TCQ row slices; refit and PACK tail)
+                                                       HIP kernels ltq_ldlq_sub per sub-block, tcq_viterbi
+                                                       two-pass tail-biting, ltq_ldlq_err / ltq_ldlq_update on
+                                                       the matrix cores across blocks: fixed-order sums)
+  refit_scales                src/liqk_v2.py:1139-1180 (the joint c_row / suh refit, as a record)
+  quantize_matrix_liqk_v2     src/liqk_v2.py:1030-1198 (single TCQ spec or TCQ row slices; refit and PACK tail)
 
-The dense linear algebra (Cholesky, triangular inverse and solves, the inter-block error GEMM, the refit
-products) runs on the device through ltq_amd.linalg and torch, i.e. as large hipBLASLt / rocBLAS GEMMs.
+The factorization and the refit's products and solve run on the device through ltq_amd.linalg and torch (MAGMA,
+hipBLASLt / rocBLAS).
 """
 from __future__ import annotations
 
@@ -111,9 +113,17 @@ def row_scale(W_rot: torch.Tensor, cfg: dict) -> Tuple[torch.Tensor, torch.Tenso
 
 @torch.no_grad()
 def _quantize_rows_tcq_ldlq(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: torch.Tensor, diag_w: torch.Tensor,
-                            spec_name: str) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Block16-LDLQ with every 16-column sub-block quantized in 16 x 16 tiles by the TCQ Viterbi. Returns
-    (d_full [M, K/256] fp16, W_hat_rot [M, K])."""
+                            spec_name: str, n_pass: int = 2,
+                            fed: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Block16-LDLQ with every 16-column sub-block quantized in 16 x 16 tiles by the TCQ Viterbi
+    (src/liqk_v2.py:877-1021, the row-scale branch; n_pass belongs to the branch without row scale and is unused).
+    Returns (d_full [M, K/256] fp16, W_hat_rot [M, K]). If fed [M, K] fp32 is given, it receives the value of every
+    weight at the moment its sub-block was quantized (the Viterbi input times d).
+
+    Per 256-column block: 16 x (two-pass tail-biting Viterbi over the M/16 tiles, ltq_ldlq_sub: the sub-block's
+    feedback into the block's working copy and the next tiles), then ltq_ldlq_err (the block's error E and its
+    reconstruction) and ltq_ldlq_update (W[:, c1:] -= E U[c0:c1, c1:], which also writes the next block's working
+    copy and first tiles). Every sum is a fixed-order fma chain, so the loop is a defined function of its inputs."""
     cfg = TCQ_CONFIG[spec_name]
     if not cfg.get("row_scale") or "K_hi" in cfg or (cfg.get("carry") and not cfg.get("tb")):
         raise NotImplementedError(f"{spec_name}: the GPU path serves the tail-biting row-scale formats")
@@ -129,60 +139,65 @@ def _quantize_rows_tcq_ldlq(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: to
     sub = cfg.get("sub", SUBBLOCK_SIZE)
     W_work = W_rot.float().clone()
     W_hat_rot = torch.empty_like(W_work)
-    d_full = torch.empty((M, nblocks), dtype=torch.float16, device=device)
     pk = None
     if PACK is not None:
         assert cfg.get("tb") and cfg.get("row_scale"), f"{spec_name}: only formats with tail-biting and d_row are written to .ltq"
         pk = {"idx": torch.empty((M, K), dtype=torch.int16, device=device),
               "gi": torch.empty((M, K), dtype=torch.uint8, device=device),
               "G": torch.empty((M, K), dtype=torch.float32, device=device)}
-    if U.stride(1) != 1:
+    if U.stride(1) != 1 or U.stride(0) % 4 or U.data_ptr() % 16:
         U = U.contiguous()
     if U_blks_inv.stride(2) != 1:
         U_blks_inv = U_blks_inv.contiguous()
+    if fed is not None:
+        assert fed.shape == (M, K) and fed.dtype == torch.float32 and fed.stride(1) == 1
     d_row, e_rb, d_rb_all = row_scale(W_rot, cfg)
+    d_full = d_rb_all.to(torch.float16)
     lib = _lib.lib()
     stream = _lib.stream_ptr()
     x_cur = torch.empty((nt, QK_K), dtype=torch.float32, device=device)
     x_nxt = torch.empty_like(x_cur)
+    w_sub = W_work[:, :QK_K].clone()      # the working copy of the block being quantized
+    E_t = torch.empty((QK_K, M), dtype=torch.float32, device=device)
     G_buf = torch.empty((M, QK_K), dtype=torch.float32, device=device) if pk is None else None
+    _check(lib.ltq_ldlq_prep(w_sub.data_ptr(), QK_K, d_rb_all.data_ptr(), nblocks, x_cur.data_ptr(), M, stream),
+           "ltq_ldlq_prep")
     for ibl in range(nblocks):
         c0, c1 = ibl * QK_K, (ibl + 1) * QK_K
-        w_blk_start = W_work[:, c0:c1].clone()
-        w_sub_work = w_blk_start.clone()
         U_blk = U[c0:c1, c0:c1]
         U_blk_inv = U_blks_inv[ibl]
-        diag_w_blk = diag_w[c0:c1]
         d_rb = d_rb_all[:, ibl]
         # per-position weights of every sub-block's tiles (t = 16 r + c -> diag_w[s0 + c]), once per block
-        wts_blk = diag_w_blk.view(NUM_SUBBLOCKS, 1, 1, SUBBLOCK_SIZE).expand(NUM_SUBBLOCKS, nt, 16, SUBBLOCK_SIZE)
+        wts_blk = diag_w[c0:c1].view(NUM_SUBBLOCKS, 1, 1, SUBBLOCK_SIZE).expand(NUM_SUBBLOCKS, nt, 16, SUBBLOCK_SIZE)
         wts_blk = wts_blk.reshape(NUM_SUBBLOCKS, nt, 16 * SUBBLOCK_SIZE)
-        G_pass = G_buf if pk is None else pk["G"][:, c0:c1]
+        G_pass, ldg = (G_buf, QK_K) if pk is None else (pk["G"][:, c0:], K)
         codes = (pk["idx"][:, c0:], pk["idx"].stride(0), pk["gi"][:, c0:], pk["gi"].stride(0)) if pk else None
-        _check(lib.ltq_ldlq_prep(w_sub_work.data_ptr(), QK_K, d_rb.data_ptr(), nblocks, x_cur.data_ptr(), M, stream),
-               "ltq_ldlq_prep")
         for ib in range(NUM_SUBBLOCKS):
-            s0, s1 = ib * SUBBLOCK_SIZE, (ib + 1) * SUBBLOCK_SIZE
+            s1 = (ib + 1) * SUBBLOCK_SIZE
             out = viterbi_ub_cuda(x_cur, lut, cfg["K"], cfg["nu"], cfg["m"], gains, sub=sub, wts=wts_blk[ib],
                                   n_cand=n_cand, tail_biting=True, tb_window=tb_window,
                                   m_extra=cfg.get("m_extra", ()), pair_parity=cfg.get("pp", False),
                                   return_code=pk is not None, _raw_code=True)
             rec, code = out if pk is not None else (out, None)
             # G, the error feedback, the next sub-block's tiles and (PACK) the code / gain index scatter
-            _check(lib.ltq_ldlq_sub(w_sub_work.data_ptr(), QK_K, rec.data_ptr(), d_rb.data_ptr(), nblocks,
+            _check(lib.ltq_ldlq_sub(w_sub.data_ptr(), QK_K, rec.data_ptr(), d_rb.data_ptr(), nblocks,
                                     U_blk_inv.data_ptr(), U_blk_inv.stride(0), U_blk.data_ptr(), U_blk.stride(0), ib,
-                                    G_pass.data_ptr(), G_pass.stride(0), x_nxt.data_ptr() if s1 < QK_K else None, M,
+                                    G_pass.data_ptr(), ldg, x_nxt.data_ptr() if s1 < QK_K else None, M,
                                     code.data_ptr() if code is not None else None,
                                     codes[0].data_ptr() if codes else None, codes[1] if codes else 0,
-                                    codes[2].data_ptr() if codes else None, codes[3] if codes else 0, stream),
-                   "ltq_ldlq_sub")
+                                    codes[2].data_ptr() if codes else None, codes[3] if codes else 0,
+                                    fed[:, c0:].data_ptr() if fed is not None else None,
+                                    fed.stride(0) if fed is not None else 0, stream), "ltq_ldlq_sub")
             x_cur, x_nxt = x_nxt, x_cur
-        best_what_row = d_rb.unsqueeze(1) * G_pass
-        W_hat_rot[:, c0:c1] = best_what_row
-        d_full[:, ibl] = d_rb.to(torch.float16)
+        # the block's reconstruction and error (W_work[:, c0:c1] still holds the block's start)
+        Wb = W_work[:, c0:]
+        _check(lib.ltq_ldlq_err(Wb.data_ptr(), K, G_pass.data_ptr(), ldg, d_rb.data_ptr(), nblocks,
+                                U_blk_inv.data_ptr(), U_blk_inv.stride(0), E_t.data_ptr(), M,
+                                W_hat_rot[:, c0:].data_ptr(), K, M, stream), "ltq_ldlq_err")
         if c1 < K:
-            err_blk = (w_blk_start - best_what_row) @ U_blk_inv
-            W_work[:, c1:].addmm_(err_blk, U[c0:c1, c1:], alpha=-1.0)
+            _check(lib.ltq_ldlq_update(W_work[:, c1:].data_ptr(), K, E_t.data_ptr(), M, U[c0:c1, c1:].data_ptr(),
+                                       U.stride(0), M, K - c1, w_sub.data_ptr(), QK_K, x_cur.data_ptr(),
+                                       d_rb_all[:, ibl + 1].data_ptr(), nblocks, stream), "ltq_ldlq_update")
     if pk is not None:
         PACK["groups"].append({"spec": spec_name, "d_row": d_row, "e": e_rb, "idx": pk["idx"], "gi": pk["gi"],
                                "G": pk["G"]})
@@ -233,8 +248,8 @@ def refit_scales(W: torch.Tensor, H: torch.Tensor, HW: torch.Tensor, U_base: tor
     W_hat H): (c_eff U_base) * suh_cand when accepted, else U_base * suh."""
     W_hat = U_base * suh.unsqueeze(0)
     HQ = W_hat @ H
-    gain_num = torch.einsum("mk,mk->m", W_hat, HW)
-    gain_den = torch.einsum("mk,mk->m", W_hat, HQ).clamp(min=1e-12)
+    gain_num = (W_hat * HW).sum(dim=1)
+    gain_den = (W_hat * HQ).sum(dim=1).clamp(min=1e-12)
     c_raw = gain_num / gain_den
     usable = torch.isfinite(c_raw) & (c_raw > 0.5) & (c_raw < 2.0)
     c_row = torch.where(usable, c_raw, torch.ones_like(c_raw))
@@ -364,7 +379,7 @@ class _MatrixJob:
 
     def relative_loss(self) -> float:
         num = float(row_proxy(self.HW, self.HQ, self.W, self.W_hat).sum().item())
-        den = float(torch.einsum("mk,mk->", self.HW, self.W).clamp(min=1e-12).item())
+        den = float((self.HW * self.W).sum().clamp(min=1e-12).item())
         return num / den
 
 

@@ -55,8 +55,8 @@ def _additive_fit(c: torch.Tensor, wgt: torch.Tensor, sweeps: int = 20) -> torch
     off = torch.zeros(c.shape[0], dtype=c.dtype, device=c.device)
     w_u, w_lb = wgt.sum(dim=0), wgt.sum(dim=1)
     for _ in range(sweeps):
-        base = torch.einsum("lu,lu->u", c - off.unsqueeze(1), wgt) / w_u
-        off = torch.einsum("lu,lu->l", c - base.unsqueeze(0), wgt) / w_lb
+        base = ((c - off.unsqueeze(1)) * wgt).sum(dim=0) / w_u
+        off = ((c - base.unsqueeze(0)) * wgt).sum(dim=1) / w_lb
     return base.unsqueeze(0) + off.unsqueeze(1)
 
 

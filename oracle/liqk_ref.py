@@ -8,7 +8,9 @@ Reference anchors (torch on the CPU, float32, the reference's order of operation
                          fp32 torch text, kept to count fp16 flips against it)
   factor_hessian_ref     src/liqk_v2.py:1066-1088
   quantize_rows_ref      src/liqk_v2.py:877-1021, row-scale branch with tail-biting formats (quant_sub at
-                         :913-921 via the C oracle's two-pass tail-biting driver)
+                         :913-921 via the C oracle's two-pass tail-biting driver; the feedback sums through
+                         oracle/ldlq_oracle.c in the kernels' fixed order)
+  ldlq_identity_residual the loop's defining identity W_rot - W_hat = E U (float64), the pin of the loop
 """
 from __future__ import annotations
 
@@ -139,56 +141,107 @@ def factor_hessian_ref(H_rot: torch.Tensor, damp: float):
     return U.float(), diag_w.float(), U_blks_inv.float()
 
 
-def quantize_rows_ref(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: torch.Tensor, diag_w: torch.Tensor, cfg: dict,
-                      gains: np.ndarray, tb_window: int = 32, n_cand: int | None = None, d_rb_all=None):
-    """(d_full fp16 [M, nblk], W_hat_rot [M, K], codes {idx int16 [M, K], gi uint8 [M, K]}, first-sub-block
-    Viterbi inputs [nt, 256]). d_rb_all may be given (the device's row scale) to compare the LDLQ loop alone."""
-    M, K = W_rot.shape
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def quantize_rows_ref(W_rot, U, U_blks_inv, diag_w, cfg: dict, gains: np.ndarray, tb_window: int = 32,
+                      n_cand: int | None = None, d_rb_all=None, mistake: str = "", trace: dict | None = None):
+    """The row quantizer's LDLQ loop (src/liqk_v2.py:948-980, row-scale branch) over the C oracle's Viterbi and
+    its LDLQ restatements (oracle/ldlq_oracle.c: fma chains in ascending order, as the kernels define the sums).
+    Returns (d_full fp16 [M, nblk], W_hat_rot [M, K], codes {idx int16, gi uint8}, fed [M, K]): fed holds every
+    weight's value when its sub-block was quantized. d_rb_all may be given ([M, nblk]); by default the row scale
+    comes from row_scale_ref. `mistake` plants one error for the tests that check the identities catch it:
+    "sign" (the sub-block feedback added instead of subtracted), "slice" (the inter-block update from the
+    factor's rows shifted by one) or "index" (the next sub-block fed from the wrong column). With a `trace`
+    dict, trace["x"] [M, K] receives the Viterbi inputs in matrix layout."""
+    L = ref.lib()
+    W = np.ascontiguousarray(W_rot.numpy() if hasattr(W_rot, "numpy") else W_rot, np.float32)
+    Uf = np.ascontiguousarray(U.numpy() if hasattr(U, "numpy") else U, np.float32)
+    Ubi = np.ascontiguousarray(U_blks_inv.numpy() if hasattr(U_blks_inv, "numpy") else U_blks_inv, np.float32)
+    dw = np.ascontiguousarray(diag_w.numpy() if hasattr(diag_w, "numpy") else diag_w, np.float32)
+    M, K = W.shape
     nt, nblocks = M // 16, K // QK_K
     n_cand = cfg.get("n_cand", 0) if n_cand is None else n_cand
     lut = np.asarray(cfg["lut"], np.float32)
     m_extra = tuple(cfg.get("m_extra", ()))
-    W_work = W_rot.float().clone()
-    W_hat_rot = torch.empty_like(W_work)
-    d_full = torch.empty((M, nblocks), dtype=torch.float16)
-    idx = torch.empty((M, K), dtype=torch.int16)
-    gim = torch.empty((M, K), dtype=torch.uint8)
     if d_rb_all is None:
-        _, _, _, d_np = row_scale_ref(W_rot, cfg)
-        d_rb_all = torch.from_numpy(d_np)
-    first_x = None
+        _, _, _, d_rb_all = row_scale_ref(W, cfg)
+    d_all = np.ascontiguousarray(d_rb_all.numpy() if hasattr(d_rb_all, "numpy") else d_rb_all, np.float32)
+    d_all = np.maximum(d_all, np.float32(1e-8))
+    W_work = W.copy()
+    W_hat = np.empty_like(W)
+    fed = np.empty_like(W)
+    xs_all = np.empty_like(W) if trace is not None else None
+    idx = np.empty((M, K), np.int16)
+    gim = np.empty((M, K), np.uint8)
+    G = np.empty((M, QK_K), np.float32)
+    E = np.empty((M, QK_K), np.float32)
     for ibl in range(nblocks):
         c0, c1 = ibl * QK_K, (ibl + 1) * QK_K
-        w_blk_start = W_work[:, c0:c1].clone()
-        U_blk = U[c0:c1, c0:c1]
-        U_blk_inv = U_blks_inv[ibl]
-        diag_w_blk = diag_w[c0:c1]
-        d_rb = d_rb_all[:, ibl].clamp(min=1e-8)
-        w_sub_work = w_blk_start.clone()
-        G_pass = torch.empty((M, QK_K), dtype=torch.float32)
-        inv_d = 1.0 / d_rb.unsqueeze(1)
+        w_sub = np.ascontiguousarray(W_work[:, c0:c1])
+        U_blk = np.ascontiguousarray(Uf[c0:c1, c0:c1])
+        if mistake == "sign":
+            U_blk = -U_blk
+        Ubi_b = Ubi[ibl]
+        d = np.ascontiguousarray(d_all[:, ibl])
+        inv = np.float32(1.0) / d
+        x = np.ascontiguousarray((w_sub[:, :SUB] * inv[:, None]).reshape(nt, 256))
+        fed_b = np.empty((M, QK_K), np.float32)
         for ib in range(QK_K // SUB):
             s0, s1 = ib * SUB, (ib + 1) * SUB
-            w_sub_orig = w_sub_work[:, s0:s1]
-            xs = (w_sub_orig * inv_d).contiguous().view(nt, 256).numpy()
-            if first_x is None:
-                first_x = xs.copy()
-            wts = np.tile(diag_w_blk[s0:s1].numpy(), 16)
-            rec, gi, ix = ref.viterbi_ub_cuda_ref(xs, lut, cfg["K"], 10, cfg["m"], gains, sub=cfg.get("sub", 16),
+            wts = np.tile(dw[c0 + s0:c0 + s1], 16)
+            if xs_all is not None:
+                xs_all[:, c0 + s0:c0 + s1] = x.reshape(M, SUB)
+            rec, gi, ix = ref.viterbi_ub_cuda_ref(x, lut, cfg["K"], 10, cfg["m"], gains, sub=cfg.get("sub", 16),
                                                   wts=wts, n_cand=n_cand, tail_biting=True, tb_window=tb_window,
                                                   m_extra=m_extra, pair_parity=int(cfg.get("pp", 0)),
                                                   return_code=True)
-            g_sub = torch.tensor(rec).view(M, SUB)
-            idx[:, c0 + s0:c0 + s1] = torch.tensor(ix).view(M, SUB).to(torch.int16)
-            gim[:, c0 + s0:c0 + s1] = torch.tensor(gi).view(M, SUB).to(torch.uint8)
-            G_pass[:, s0:s1] = g_sub
-            if s1 < QK_K:
-                err_sub = (w_sub_orig - d_rb.unsqueeze(1) * g_sub) @ U_blk_inv[s0:s1, s0:s1]
-                w_sub_work[:, s1:] -= err_sub @ U_blk[s0:s1, s1:]
-        best_what_row = d_rb.unsqueeze(1) * G_pass
-        W_hat_rot[:, c0:c1] = best_what_row
-        d_full[:, ibl] = d_rb.to(torch.float16)
+            rec = np.ascontiguousarray(rec, np.float32)
+            idx[:, c0 + s0:c0 + s1] = np.asarray(ix).reshape(M, SUB).astype(np.int16)
+            gim[:, c0 + s0:c0 + s1] = np.asarray(gi).reshape(M, SUB).astype(np.uint8)
+            x_next = np.empty((nt, 256), np.float32)
+            L.ltq_oracle_ldlq_sub(_ptr(w_sub), QK_K, _ptr(rec), _ptr(d), 1, _ptr(Ubi_b), QK_K, _ptr(U_blk), QK_K, ib,
+                                  _ptr(G), QK_K, _ptr(x_next) if s1 < QK_K else None, M, _ptr(fed_b), QK_K)
+            if mistake == "index" and s1 < QK_K:
+                j = min(s1 + 1, QK_K - SUB)
+                x_next = np.ascontiguousarray((w_sub[:, j:j + SUB] * inv[:, None]).reshape(nt, 256))
+            x = x_next
+        fed[:, c0:c1] = fed_b
+        wh = np.empty((M, QK_K), np.float32)
+        ws = np.ascontiguousarray(W_work[:, c0:c1])
+        L.ltq_oracle_ldlq_err(_ptr(ws), QK_K, _ptr(G), QK_K, _ptr(d), 1, _ptr(Ubi_b), QK_K, _ptr(E), QK_K, _ptr(wh),
+                              QK_K, M)
+        W_hat[:, c0:c1] = wh
         if c1 < K:
-            err_blk = (w_blk_start - best_what_row) @ U_blk_inv
-            W_work[:, c1:] -= err_blk @ U[c0:c1, c1:]
-    return d_full, W_hat_rot, {"idx": idx, "gi": gim}, first_x
+            r0 = c0 + 1 if mistake == "slice" else c0   # c1 < K, so rows r0 .. r0 + 255 exist
+            Up = np.ascontiguousarray(Uf[r0:r0 + QK_K, c1:])
+            rest = np.ascontiguousarray(W_work[:, c1:])
+            L.ltq_oracle_ldlq_update(_ptr(rest), K - c1, _ptr(E), QK_K, _ptr(Up), K - c1, M, K - c1)
+            W_work[:, c1:] = rest
+    d_full = d_all.astype(np.float16)
+    if trace is not None:
+        trace["x"] = xs_all
+    return d_full, W_hat, {"idx": idx, "gi": gim}, fed
+
+
+def ldlq_identity_residual(W_rot, W_hat, fed, U, U_blks_inv):
+    """The defining identity of the LDLQ loop, in float64: with E_j = (fed_j - W_hat_j) U_jj^-1 for every 16-column
+    sub-block j (U_jj^-1 the diagonal 16 x 16 block of the block inverse), W_rot - W_hat = E U exactly. Returns
+    (R = (W_rot - W_hat) - E U, B = |W_rot| + |E| |U|): an fp32 implementation of the loop leaves |R| within a
+    few hundred units of roundoff of B, while a wrong sign, slice or feedback index leaves residuals of the
+    size of B itself."""
+    Wr = np.asarray(W_rot, np.float64)
+    Wh = np.asarray(W_hat, np.float64)
+    F = np.asarray(fed, np.float64)
+    Ud = np.asarray(U, np.float64)
+    Ubi = np.asarray(U_blks_inv, np.float64)
+    M, K = Wr.shape
+    E = np.empty_like(Wr)
+    for c0 in range(0, K, SUB):
+        b, s0 = c0 // QK_K, c0 % QK_K
+        Uinv_jj = Ubi[b, s0:s0 + SUB, s0:s0 + SUB]
+        E[:, c0:c0 + SUB] = (F[:, c0:c0 + SUB] - Wh[:, c0:c0 + SUB]) @ Uinv_jj
+    R = (Wr - Wh) - E @ Ud
+    B = np.abs(Wr) + np.abs(E) @ np.abs(Ud)
+    return R, B

@@ -46,6 +46,13 @@ def lib():
         L.ltq_oracle_lut_subs.argtypes = [vp] * 4 + [ctypes.c_long, ctypes.c_float, ctypes.c_float, ci]
         L.ltq_oracle_labels.restype = None
         L.ltq_oracle_labels.argtypes = [ci] * 6 + [vp]
+        cl = ctypes.c_long
+        L.ltq_oracle_ldlq_sub.restype = None
+        L.ltq_oracle_ldlq_sub.argtypes = [vp, cl, vp, vp, cl, vp, cl, vp, cl, ci, vp, cl, vp, cl, vp, cl]
+        L.ltq_oracle_ldlq_err.restype = None
+        L.ltq_oracle_ldlq_err.argtypes = [vp, cl, vp, cl, vp, cl, vp, cl, vp, cl, vp, cl, cl]
+        L.ltq_oracle_ldlq_update.restype = None
+        L.ltq_oracle_ldlq_update.argtypes = [vp, cl, vp, cl, vp, cl, cl, cl]
         L.ltq_brute_force.restype = ctypes.c_double
         L.ltq_brute_force.argtypes = [vp] + [ci] * 12 + [vp, vp, vp]
         _LIB = L

@@ -3,8 +3,9 @@
 
 CPU: the oracle's torch restatement of the row scale against its float64 definition, and of the factors
 against their defining identities (U^T U = H^-1 after damping, block inverses).
-GPU: the HIP row scale and LDLQ kernels against the restatement, the whole TCQ275X2 row quantizer against the
-CPU oracle driving the C Viterbi oracle, and PACK -> .ltq bytes -> decode equal to the quantizer's fields.
+GPU: the HIP row scale against the oracle's definition bit for bit; the c_row / suh refit against its closed
+forms and float64 recomputations; PACK -> .ltq bytes -> decode equal to the quantizer's fields. The LDLQ loop
+is pinned in tests/test_ldlq.py.
 """
 import numpy as np
 import pytest
@@ -111,86 +112,93 @@ def test_gpu_row_scale(M, K, seed):
     assert np.array_equal(d.cpu().numpy().view(np.uint32), d_all_ref.view(np.uint32))
 
 
-@pytest.mark.gpu
-def test_gpu_ldlq_sub_matches_float64():
-    from ltq_amd import _lib
-    g = torch.Generator().manual_seed(4)
-    M = 64
-    wk = torch.randn((M, 256), generator=g)
-    rec = torch.randn((M // 16, 256), generator=g)
-    d = torch.rand(M, generator=g) + 0.5
-    U = torch.triu(torch.randn((256, 256), generator=g) * 0.1) + torch.eye(256)
-    Ui = torch.linalg.inv(U).contiguous()  # LAPACK may return column-major strides
-    for ib in (0, 7, 15):
-        s0, s1 = 16 * ib, 16 * ib + 16
-        wk_d, G = wk.to(DEV).clone(), torch.zeros((M, 256), device=DEV)
-        xn = torch.zeros((M // 16, 256), device=DEV)
-        rec_d, d_d, Ui_d, U_d = rec.to(DEV), d.to(DEV), Ui.to(DEV), U.to(DEV)  # alive across the call
-        print(f"ldlq_sub ib={ib}", flush=True)
-        code = torch.randint(0, 1 << 19, (M // 16, 256), generator=g, dtype=torch.int32)
-        code_d = code.to(DEV)
-        idx = torch.full((M, 512), -1, dtype=torch.int16, device=DEV)
-        gi = torch.full((M, 512), 255, dtype=torch.uint8, device=DEV)
-        rc = _lib.lib().ltq_ldlq_sub(wk_d.data_ptr(), 256, rec_d.data_ptr(), d_d.data_ptr(), 1, Ui_d.data_ptr(), 256,
-                                     U_d.data_ptr(), 256, ib, G.data_ptr(), 256, xn.data_ptr(), M, code_d.data_ptr(),
-                                     idx[:, 256:].data_ptr(), 512, gi[:, 256:].data_ptr(), 512, _lib.stream_ptr())
-        assert rc == 0
-        torch.cuda.synchronize()
-        cv = code.view(M, 16)
-        assert torch.equal(idx.cpu()[:, 256 + s0:256 + s1], (cv & 0xFFFF).to(torch.int16))
-        assert torch.equal(gi.cpu()[:, 256 + s0:256 + s1], (cv >> 16).to(torch.uint8))
-        assert int((idx.cpu() != -1).sum()) == M * 16 and int((gi.cpu() != 255).sum()) <= M * 16
-        g_sub = rec.view(M, 16).double()
-        err = (wk[:, s0:s1].double() - d.double().unsqueeze(1) * g_sub) @ Ui.double()[s0:s1, s0:s1]
-        ref = wk.double().clone()
-        ref[:, s1:] -= err @ U.double()[s0:s1, s1:]
-        assert torch.allclose(wk_d.cpu().double(), ref, rtol=1e-5, atol=1e-5)
-        assert torch.equal(G.cpu()[:, s0:s1], rec.view(M, 16))
-        if s1 < 256:
-            xr = (wk_d.cpu()[:, s1:s1 + 16] * (1.0 / d).unsqueeze(1)).contiguous().view(M // 16, 256)
-            assert torch.equal(xn.cpu(), xr)  # the same fp32 products as the reference's w * inv_d
-
-
-@pytest.mark.gpu
-@pytest.mark.parametrize("spec,identity_h", [("TCQ275X2", False), ("TCQ275X", False), ("TCQ25X", False),
-                                             ("TCQ375X", False), ("TCQ3X3", True)])
-def test_gpu_quantize_rows_vs_oracle(spec, identity_h):
-    """Rows [64, 512] (C3 formats with a real Hessian; C2's TCQ3X3 with gain candidates and H = I): the GPU
-    quantizer against the CPU oracle on the same row scale. The first sub-block's inputs are identical, so its
-    codes are bit-exact; afterwards the error feedback sums round differently (FMA vs the oracle's torch
-    matmul), so codes may differ at near-ties only."""
-    from oracle import liqk_ref
-    from ltq_amd import liqk, rotation
-    from ltq_amd.formats import TCQ_CONFIG, make_format
-    cfg = TCQ_CONFIG[spec]
-    M, K = 64, 512
-    W, H = _synthetic(M, K)
+def _refit_inputs(M=64, K=512, seed=11, identity_h=False):
+    g = torch.Generator().manual_seed(seed)
+    W, H = _synthetic(M, K, seed=seed)
     if identity_h:
         H = torch.eye(K)
+    suh = ((torch.rand(K, generator=g) * 1.5 + 0.5) * torch.sign(torch.randn(K, generator=g))).half().float()
+    noise = 1 + 0.1 * torch.randn((M, K), generator=g)
+    W_hat = W * noise
+    W_hat[0] = W[0] * 0.8     # c_row = 1.25
+    W_hat[1] = W[1] * 3.0     # c_row ~ 1/3: outside (0.5, 2), replaced by 1
+    W_hat[2] = W[2] * 0.25    # c_row ~ 4: replaced by 1
+    U_base = W_hat / suh
+    d = (torch.rand((M, K // 256), generator=g) * 0.02 + 0.01).half()
+    rw = (torch.rand(M, generator=g) + 0.5)
+    return W, H, U_base, suh, d, rw
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("weighted", [False, True])
+def test_gpu_refit_pins(weighted):
+    """refit_scales against what fixes it: c_row is the per-row ratio <W_hat, W H> / <W_hat, W_hat H> (float64)
+    with the (0.5, 2) rule, d_new = fp16(d c_row) exactly, the normal equations (A, b) equal their float64
+    definition, the solve's output satisfies them to fp32 backward error, the candidate follows the fp16 /
+    validity rule exactly, and the two losses and the acceptance agree with their float64 recomputation."""
+    from ltq_amd import liqk, rotation
+    W, H, U_base, suh, d, rw = _refit_inputs()
+    rw_n = rotation.normalized_row_weights(rw.to(DEV)).float() if weighted else None
     Wd, Hd = W.to(DEV), H.to(DEV)
-    W_rot, H_rot, _ = rotation.compute_optimal_suh(Wd, Hd, seed=1337)
-    U, diag_w, Ub_inv = liqk.factor_hessian(H_rot, 0.2)
-    print(f"quantize rows 64 x 512 {spec}", flush=True)
-    liqk.PACK = {"groups": []}
-    try:
-        d_full, W_hat = liqk._quantize_rows_tcq_ldlq(W_rot, U, Ub_inv, diag_w, spec)
-        grp = liqk.PACK["groups"].pop()
-    finally:
-        liqk.PACK = None
+    HW = Wd @ Hd
+    print(f"refit pins weighted={weighted}", flush=True)
+    rec, W_hat_out, HQ_out = liqk.refit_scales(Wd, Hd, HW, U_base.to(DEV), suh.to(DEV), d.to(DEV), rw_n, keep=True)
     torch.cuda.synchronize()
-    _, _, d_dev = liqk.row_scale(W_rot, cfg)
-    f = make_format(spec)
-    dr, Wh_ref, codes, _ = liqk_ref.quantize_rows_ref(W_rot.cpu(), U.cpu(), Ub_inv.cpu(), diag_w.cpu(), cfg,
-                                                      f.gain_tab, d_rb_all=d_dev.cpu())
-    idx, gi = grp["idx"].cpu(), grp["gi"].cpu()
-    assert torch.equal(idx[:, :16], codes["idx"][:, :16]) and torch.equal(gi[:, :16], codes["gi"][:, :16])
-    agree = (idx == codes["idx"]).float().mean().item()
-    assert agree >= 0.98, agree
-    Wr = W_rot.cpu()
-    mse_gpu = (Wr - W_hat.cpu()).square().mean().item()
-    mse_ref = (Wr - Wh_ref).square().mean().item()
-    assert abs(mse_gpu - mse_ref) <= 0.02 * mse_ref, (mse_gpu, mse_ref)
-    assert torch.equal(d_full.cpu(), dr)
+    W64, H64, Ub64, s64 = W.double(), H.double(), U_base.double(), suh.double()
+    Wh64 = Ub64 * s64
+    c64 = (Wh64 * (W64 @ H64)).sum(1) / (Wh64 * (Wh64 @ H64)).sum(1)
+    c_raw = rec.c_raw.cpu().double()
+    assert torch.allclose(c_raw, c64, rtol=2e-4), float(((c_raw - c64) / c64).abs().max())
+    assert abs(float(c_raw[0]) - 1.25) < 1e-4 and float(rec.c_row[1]) == 1.0 and float(rec.c_row[2]) == 1.0
+    ok = torch.isfinite(rec.c_raw) & (rec.c_raw > 0.5) & (rec.c_raw < 2.0)
+    assert torch.equal(rec.c_row, torch.where(ok, rec.c_raw, torch.ones_like(rec.c_raw)))
+    assert torch.equal(rec.d_new.cpu(), (d.float() * rec.c_row.cpu().unsqueeze(1)).half())
+    assert torch.allclose(rec.c_eff.cpu().double(), (rec.d_new.cpu().double() / d.double()).mean(1), rtol=1e-6)
+    # normal equations
+    Us = Ub64 * rec.c_eff.cpu().double().unsqueeze(1)
+    Uw = Us if rw_n is None else Us * rw_n.cpu().double().unsqueeze(1)
+    A64 = (Uw.T @ Us) * H64
+    A64.diagonal().add_(1e-3 * A64.diagonal().mean())
+    b64 = (Uw * (W64 @ H64)).sum(0)
+    A_low = torch.tril(rec.A.cpu().double())
+    assert float((A_low - torch.tril(A64)).abs().max()) <= 1e-4 * float(A64.abs().max())
+    assert torch.allclose(rec.b.cpu().double(), b64, rtol=1e-3, atol=1e-4 * float(b64.abs().max()))
+    A_sys = A_low + torch.tril(A_low, -1).T            # the system the solver was handed
+    sv = rec.s_solved.cpu().double()
+    resid = float((A_sys @ sv - rec.b.cpu().double()).abs().max())
+    scale = float(A_sys.abs().sum(1).max() * sv.abs().max())
+    print(f"refit solve: residual {resid / scale:.2e} of ||A|| ||s||", flush=True)
+    assert resid <= 1e-5 * scale
+    s16 = rec.s_solved.half().float()
+    good = torch.isfinite(s16) & (s16.abs() > 0.05) & (s16.abs() < 10.0)
+    assert torch.equal(rec.suh_cand, torch.where(good, s16, suh.to(DEV)))
+    # losses in float64 and the acceptance
+    wt = torch.ones(W.shape[0], dtype=torch.float64) if rw_n is None else rw_n.cpu().double()
+    loss_b = float((((W64 - Wh64) @ H64 * (W64 - Wh64)).sum(1) * wt).sum())
+    Wc = Us * rec.suh_cand.cpu().double()
+    loss_c = float((((W64 - Wc) @ H64 * (W64 - Wc)).sum(1) * wt).sum())
+    tol = 1e-3 * max(abs(loss_b), abs(loss_c))
+    assert abs(rec.loss_base - loss_b) <= tol and abs(rec.loss_cand - loss_c) <= tol
+    if abs(loss_b - loss_c) > 2 * tol:
+        assert rec.accepted == (loss_c < loss_b)
+    assert rec.accepted == (rec.loss_cand < rec.loss_base)
+    chosen = (Us.float() * rec.suh_cand.cpu()) if rec.accepted else (U_base * suh)
+    assert torch.allclose(W_hat_out.cpu(), chosen, rtol=1e-6, atol=1e-9)
+
+
+@pytest.mark.gpu
+def test_gpu_refit_column_scale_closed_form():
+    """With H = I the normal matrix is diagonal: s_j = <U_w[:, j], W[:, j]> / (<U_w[:, j], U_s[:, j]> + ridge),
+    ridge = 1e-3 mean of the diagonal."""
+    from ltq_amd import liqk
+    W, H, U_base, suh, d, _ = _refit_inputs(identity_h=True, seed=12)
+    Wd, Hd = W.to(DEV), H.to(DEV)
+    rec, _, _ = liqk.refit_scales(Wd, Hd, Wd @ Hd, U_base.to(DEV), suh.to(DEV), d.to(DEV), None)
+    torch.cuda.synchronize()
+    Us = U_base.double() * rec.c_eff.cpu().double().unsqueeze(1)
+    n = (Us * Us).sum(0)
+    s = (Us * W.double()).sum(0) / (n + 1e-3 * n.mean())
+    assert torch.allclose(rec.s_solved.cpu().double(), s, rtol=1e-5, atol=1e-6)
 
 
 @pytest.mark.gpu
