@@ -120,6 +120,99 @@ def read_traffic():
     return None
 
 
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+MFMA_FP32_PEAK_TFLOPS = 157.3
+
+
+class KernelTimer:
+    """HIP events around the calls of selected product functions inside the timed steps, on the current stream
+    (the stream the kernels are launched on). Each record is (name, start, end, algorithmic bytes, flops)."""
+
+    def __init__(self):
+        self.records = []
+        self.active = False
+        self._undo = []
+
+    def _wrap(self, owner, attr, name_fn):
+        import torch
+        orig = getattr(owner, attr)
+
+        def timed(*a, **k):
+            if not self.active:
+                return orig(*a, **k)
+            st = torch.cuda.current_stream()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            out = orig(*a, **k)
+            e1.record(st)
+            name, nbytes, flops = name_fn(a, k, out)
+            if name:
+                self.records.append((name, e0, e1, nbytes, flops))
+            return out
+
+        setattr(owner, attr, timed)
+        self._undo.append((owner, attr, orig))
+
+    def install(self):
+        from ltq_amd import _lib, liqk, ltq_file, rotation
+
+        def rows_fn(a, k, out):
+            x = a[0]
+            n = x.numel()
+            tag = "fwht_rows_W" if x.dtype != out.dtype else ("fwht_rows_H" if x.shape[0] == x.shape[1] else "")
+            return tag, n * (x.element_size() + 4), 0
+
+        def cols_fn(a, k, out):
+            x = a[0]
+            return ("fwht_cols_H" if x.shape[0] == x.shape[1] else ""), x.numel() * 8, 0
+
+        def scale_fn(a, k, out):
+            W = a[0]
+            return "row_scale", W.numel() * 4 + W.shape[0] * (4 + 5 * (W.shape[1] // 256)), 0
+
+        def pack_fn(a, k, out):
+            idx = a[0]
+            return "pack_slice", idx.numel() * 3 + out.numel(), 0
+
+        self._wrap(rotation, "fwht_rows", rows_fn)
+        self._wrap(rotation, "fwht_cols", cols_fn)
+        self._wrap(liqk, "row_scale", scale_fn)
+        self._wrap(ltq_file, "pack_slice_device", pack_fn)
+
+        def upd_fn(a, k, out):
+            M, N = a[6], a[7]
+            return "ldlq_update", 8 * M * N + 4 * 256 * (N + M), 2.0 * M * 256 * N
+
+        self._wrap(_lib.lib(), "ltq_ldlq_update", upd_fn)
+
+    def uninstall(self):
+        for owner, attr, orig in reversed(self._undo):
+            setattr(owner, attr, orig)
+        self._undo = []
+
+    def summary(self, steps):
+        """{name: {ms per step, GB/s, HBM fraction (and TFLOP/s, MFMA fraction)}} over the timed steps."""
+        agg = {}
+        for name, e0, e1, nbytes, flops in self.records:
+            t = e0.elapsed_time(e1) * 1e-3
+            a = agg.setdefault(name, [0.0, 0.0, 0.0, 0])
+            a[0] += t
+            a[1] += nbytes
+            a[2] += flops
+            a[3] += 1
+        out = {}
+        for name, (t, nb, fl, n) in agg.items():
+            gbs = nb / t / 1e9
+            d = {"calls_per_step": n // steps, "ms_per_step": round(t / steps * 1e3, 3),
+                 "algorithmic_bytes_per_call": int(nb / n), "gb_s": round(gbs, 1),
+                 "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+            if fl:
+                d["tflop_s"] = round(fl / t / 1e12, 1)
+                d["frac_mfma_fp32"] = round(fl / t / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4)
+            out[name] = d
+        return out
+
+
 def cpu_baseline(tiles, wts, budget_s):
     """The C oracle (OpenMP over tiles) on the first sub-blocks, in quantization order, until budget_s is spent."""
     import numpy as np
@@ -237,6 +330,117 @@ def run_rings(args):
     print(json.dumps(res), flush=True)
 
 
+C4_EXPERTS, C4_HIDDEN, C4_INTER, C4_ACT_ROWS = 128, 2048, 768, 256
+C4_FORMAT = "TCQ275Y3"  # K=3 D4, 16-subset labels, 3-bit gains over 4 candidates (closed-form table)
+
+
+def prepare_experts(dev, n_exp):
+    """C4: per expert the fused gate_up_proj [2 x 768, 2048] and down_proj [2048, 768], bf16 Student-t(5) x 0.02,
+    and their Hessians from 256 N(0, 1) activation rows each (2048- and 768-dim), accumulated by
+    ltq_cov_accumulate (seeds: weights 10 + e, activations 20000 + e). Returns (gate_up, H_in, down, H_mid,
+    H-build milliseconds)."""
+    import torch
+    from ltq_amd.hessian import CovAccumulator
+    gu, H_in, dn, H_mid = [], [], [], []
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_h = 0.0
+    for e in range(n_exp):
+        g = torch.Generator(device=dev).manual_seed(10 + e)
+        gu.append((student_t((2 * C4_INTER, C4_HIDDEN), g, dev) * 0.02).to(torch.bfloat16))
+        dn.append((student_t((C4_HIDDEN, C4_INTER), g, dev) * 0.02).to(torch.bfloat16))
+        ga = torch.Generator(device=dev).manual_seed(20000 + e)
+        xs = [torch.randn((C4_ACT_ROWS, k), generator=ga, device=dev).to(torch.bfloat16) for k in (C4_HIDDEN, C4_INTER)]
+        ev0.record()
+        hs = []
+        for x in xs:
+            acc = CovAccumulator()
+            acc.add(x)
+            hs.append(acc.get())
+        ev1.record()
+        torch.cuda.synchronize()
+        t_h += ev0.elapsed_time(ev1)
+        H_in.append(hs[0])
+        H_mid.append(hs[1])
+    return gu, H_in, dn, H_mid, t_h
+
+
+def run_experts(args):
+    """--workload c4: one step = the 128 experts' gate_up_proj and down_proj through quantize_experts with PACK
+    (per-expert rotation, factors and refit; the row quantizer of all experts of one shape in shared Viterbi
+    launches) plus every expert's .ltq slice packing."""
+    import torch
+    from ltq_amd import liqk, ltq_file, moe, tcq_proto
+    from ltq_amd.formats import TCQ_CONFIG, make_format
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    n_exp = args.experts or C4_EXPERTS
+    gu, H_in, dn, H_mid, t_h = prepare_experts(dev, n_exp)
+    f = make_format(C4_FORMAT)
+    seeds_gu = [moe.expert_seed(0, f"gu{e}") for e in range(n_exp)]
+    seeds_dn = [moe.expert_seed(0, f"dn{e}") for e in range(n_exp)]
+
+    def step():
+        liqk.PACK = {}
+        try:
+            out_gu, fl_gu = moe.quantize_experts(gu, H_in, C4_FORMAT, seeds_gu, damp=DAMP / 10)
+            out_dn, fl_dn = moe.quantize_experts(dn, H_mid, C4_FORMAT, seeds_dn, damp=DAMP / 10)
+        finally:
+            liqk.PACK = None
+        packed = [ltq_file.pack_slice_device(m["idx"], m["gi"], f) for m in fl_gu + fl_dn]
+        return out_gu, out_dn, packed
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    tcq_proto.LAUNCH_EVENTS, tcq_proto.LAUNCH_SAMPLE, tcq_proto._launch_count = [], 1, 0
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out_gu, out_dn, packed = step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    evs, tcq_proto.LAUNCH_EVENTS = tcq_proto.LAUNCH_EVENTS, None
+    durs = [a.elapsed_time(b) * 1e-3 for a, b in evs]
+    cfg = TCQ_CONFIG[C4_FORMAT]
+    G = cfg["n_cand"]
+    # launches alternate pass 1 (64 steps) and pass 2 (256 steps); gate_up launches cover n_exp x 96 tiles,
+    # down launches n_exp x 128 tiles
+    n_gu = 2 * (C4_HIDDEN // 256) * 16
+    ops = 0.0
+    for i in range(len(durs)):
+        k = i % (n_gu + 2 * (C4_INTER // 256) * 16)
+        tiles = n_exp * (2 * C4_INTER // 16 if k < n_gu else C4_HIDDEN // 16)
+        ops += tiles * (2 * TB_WINDOW if i % 2 == 0 else 256) * LANE_OPS_PER_STEP[2] * 1024 * G
+    t_vit = sum(durs)
+    achieved = ops / t_vit / 1e12
+    weights = n_exp * (2 * C4_INTER * C4_HIDDEN + C4_HIDDEN * C4_INTER)
+    value = weights / (dt / args.steps) / 1e6
+    rel = [r for _, _, r in out_gu + out_dn]
+    res = {
+        "metric": f"Mweights/s quantized (C4 MoE expert batch: {n_exp} experts x gate_up 1536x2048 + down 2048x768, "
+                  f"K=3 D4 16-subset, 4 gain candidates) on 1 GPU; % VALU ACS roofline",
+        "value": round(value, 3), "unit": "Mweights/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt / args.steps * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic, generated on the device (Student-t(5)*0.02 bf16 experts, per-expert Hessians from 256 "
+                "N(0,1) bf16 activation rows; seeds 10+e / 20000+e)",
+        "config": {"workload": f"C4 {n_exp} experts: gate_up_proj [1536, 2048] and down_proj [2048, 768] per expert, "
+                               f"{C4_FORMAT} (K=3 D4, masks 359/40/475, h=3, n_cand=4) tail-biting tb_window=32, "
+                               f"damping 0.2, LDLQ on; one step = quantize_experts for both shapes (one Viterbi "
+                               f"launch per sub-block over all experts' tiles) with PACK + .ltq slices",
+                   "format": C4_FORMAT, "experts": n_exp, "parallelism": "single GPU"},
+        "roofline": {"bound": "valu", "timed_on": "HIP events around every Viterbi launch of the timed steps",
+                     "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
+                     "unit": "TFLOP/s (fp32 VALU lane-ops/s x 1e-12)", "frac": round(achieved / VALU_PEAK_TOPS, 4),
+                     "traffic": None, "kernel": "tcq_viterbi_kernel<10,2,2,16,1>",
+                     "viterbi_ms_per_step": round(t_vit / args.steps * 1e3, 2),
+                     "viterbi_launches_per_step": len(durs) // args.steps},
+        "breakdown": {"mweights_s_viterbi": round(weights / (t_vit / args.steps) / 1e6, 3),
+                      "h_build_ms": round(t_h, 2), "proxy_rel_loss_mean": round(sum(rel) / len(rel), 6),
+                      "packed_bytes": int(sum(p.numel() for p in packed))},
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -247,8 +451,10 @@ def main():
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="profiling runs: first copy this many MiB device-to-device (a known-size kernel that "
                          "calibrates the FETCH_SIZE / WRITE_SIZE counters)")
-    ap.add_argument("--workload", choices=("c3", "c5"), default="c3",
-                    help="c3: the headline matrix quantizer (default); c5: the ring table (an extra line on request)")
+    ap.add_argument("--workload", choices=("c3", "c4", "c5"), default="c3",
+                    help="c3: the headline matrix quantizer (default); c4: the MoE expert batch; c5: the ring table "
+                         "(extra lines on request)")
+    ap.add_argument("--experts", type=int, default=0, help="c4: number of experts (default 128)")
     ap.add_argument("--rows", type=int, default=0, help="c5: table rows (default 262144)")
     ap.add_argument("--format", default="", help="c5: ring format (default TCQ375X, K=4 D4; TCQ4X as published)")
     args = ap.parse_args()
@@ -260,6 +466,8 @@ def main():
         sys.exit("--cols must be a positive multiple of 256")
     if args.workload == "c5":
         return run_rings(args)
+    if args.workload == "c4":
+        return run_experts(args)
 
     import torch
     from ltq_amd import liqk, ltq_file, tcq_proto
@@ -290,11 +498,14 @@ def main():
         liqk._mark("pack")
         return packed, pm, q, rel
 
+    timer = KernelTimer()
+    timer.install()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     # stage marks every step; Viterbi launch events on one sub-block in 16 (both passes), so the event records
-    # do not perturb the launch stream
+    # do not perturb the launch stream; events around the rotation, row-scale, pack and LDLQ-update calls
+    timer.active = True
     liqk.STAGE_EVENTS, tcq_proto.LAUNCH_EVENTS = [], []
     tcq_proto.LAUNCH_SAMPLE, tcq_proto._launch_count = 16, 0
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -308,6 +519,9 @@ def main():
     dt = time.perf_counter() - t0
     stage_ev, launch_ev = liqk.STAGE_EVENTS, tcq_proto.LAUNCH_EVENTS
     liqk.STAGE_EVENTS = tcq_proto.LAUNCH_EVENTS = None
+    timer.active = False
+    kernels = timer.summary(args.steps)
+    timer.uninstall()
 
     ms_step = dt / args.steps * 1e3
     weights = rows * cols
@@ -355,6 +569,8 @@ def main():
                       "proxy_rel_loss": round(rel, 6),
                       "packed_bytes": int(packed.numel())},
         "h_build": h_build,
+        "hbm": {k: v for k, v in kernels.items() if k != "ldlq_update"},
+        "ldlq_update": kernels.get("ldlq_update"),
     }
     if args.cpu_seconds > 0:
         nsub = 16

@@ -135,27 +135,35 @@ int ltq_ldlq_prep(const float* wk, long ldw, const float* d, long ldd, float* x,
  * index) is not null, the PACK fields of the sub-block are written as well: idx[:, s0:s1] = code & 0xFFFF (int16,
  * row stride ld_idx) and gi[:, s0:s1] = code >> 16 (uint8, row stride ld_gi), the torch scatter of
  * src/liqk_v2.py:919-921; idx and gi point at the block's first column. If fed is not null, fed[:, s0:s1] (row
- * stride ld_fed, pointing at the block's first column) receives wk[:, s0:s1] as the sub-block's Viterbi saw it. */
+ * stride ld_fed, pointing at the block's first column) receives wk[:, s0:s1] as the sub-block's Viterbi saw it.
+ * Stacked matrices (rows_per_mat > 0, a multiple of 16 dividing M; 0 = one matrix): rows [m R, (m + 1) R) belong
+ * to matrix m, whose factors are uinv + m * uinv_ms and ublk + m * ublk_ms (the MoE expert batch). */
 int ltq_ldlq_sub(float* wk, long ldw, const float* rec, const float* d, long ldd, const float* uinv, long ldi,
                  const float* ublk, long ldu, int ib, float* G, long ldg, float* xnext, long M, const int* code,
-                 int16_t* idx, long ld_idx, uint8_t* gi, long ld_gi, float* fed, long ld_fed, void* stream);
+                 int16_t* idx, long ld_idx, uint8_t* gi, long ld_gi, float* fed, long ld_fed, long rows_per_mat,
+                 long uinv_ms, long ublk_ms, void* stream);
 
 /* Error of a finished 256-column block (src/liqk_v2.py:972-978): what[:, 0:256] = d * G (the block's
  * reconstruction, if what is not null) and E = (wstart - d * G) @ uinv, stored transposed: et[j * ld_et + i]
  * = E[i][j] (et is [256, M]). Each E entry is the fma chain over k = 0..255 ascending from 0 (fp32 MFMA, whose
  * four-term steps are that chain). wstart, G: [M, 256] (row strides ldw, ldg); d: [M] (stride ldd); uinv:
- * [256, 256]. M % 16 == 0; every matrix pointer 16-byte aligned and every row stride a multiple of 4. */
+ * [256, 256]. M % 16 == 0; every matrix pointer 16-byte aligned and every row stride a multiple of 4. Stacked
+ * matrices: rows_per_mat > 0 (a multiple of 128 dividing M) gives rows [m R, (m + 1) R) the factor uinv + m *
+ * uinv_ms (uinv_ms a multiple of 4); 0 = one matrix. */
 int ltq_ldlq_err(const float* wstart, long ldw, const float* G, long ldg, const float* d, long ldd, const float* uinv,
-                 long ldi, float* et, long ld_et, float* what, long ld_what, long M, void* stream);
+                 long ldi, float* et, long ld_et, float* what, long ld_what, long M, long rows_per_mat, long uinv_ms,
+                 void* stream);
 
 /* Update of the columns right of a finished block (src/liqk_v2.py:979): w[:, 0:N] -= E @ u[0:256, 0:N] with E
  * given transposed (et [256, M], row stride ld_et), each product the fma chain over k = 0..255 ascending from 0
  * (fp32 MFMA), then w - acc. Replaces the reference's cuBLAS GEMM, whose order is not fixed. Optionally also the
  * next block's working copy wsub[:, 0:256] = the updated w[:, 0:256] and its first Viterbi tiles xnext [M/16, 256]
  * (t = 16 r + c) = w[:, 0:16] * (1 / dnext). M % 16 == 0, N % 128 == 0 (N >= 256 with wsub); et and u 16-byte
- * aligned with row strides a multiple of 4. */
+ * aligned with row strides a multiple of 4. Stacked matrices as ltq_ldlq_err: rows [m R, (m + 1) R) are updated
+ * with u + m * u_ms. */
 int ltq_ldlq_update(float* w, long ldw, const float* et, long ld_et, const float* u, long ldu, long M, long N,
-                    float* wsub, long ld_wsub, float* xnext, const float* dnext, long ld_dnext, void* stream);
+                    float* wsub, long ld_wsub, float* xnext, const float* dnext, long ld_dnext, long rows_per_mat,
+                    long u_ms, void* stream);
 
 /* Input-covariance accumulation, the _CovAccumulator.add of src/liqk_v2.py:218-228 for bf16 (f16 = 0) or fp16
  * (f16 = 1) activations: H += X^T X for X [n, K] (element type 16-bit, row stride ldx >= K), fp32 accumulation

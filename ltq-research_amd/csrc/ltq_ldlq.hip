@@ -79,7 +79,8 @@ __global__ __launch_bounds__(256) void ldlq_sub_kernel(float* __restrict__ wk, l
                                                        float* __restrict__ xnext, long M,
                                                        const int* __restrict__ code, int16_t* __restrict__ idx,
                                                        long ld_idx, uint8_t* __restrict__ gi, long ld_gi,
-                                                       float* __restrict__ fed, long ld_fed)
+                                                       float* __restrict__ fed, long ld_fed, long tiles_per_mat,
+                                                       long uinv_ms, long ublk_ms)
 {
     __shared__ float s_err[16][17];
     __shared__ float s_d[16];
@@ -87,6 +88,11 @@ __global__ __launch_bounds__(256) void ldlq_sub_kernel(float* __restrict__ wk, l
     const long row0 = (long)blockIdx.x * 16, row = row0 + r;
     if (row0 >= M) return;
     const int s1 = s0 + 16;
+    if (tiles_per_mat > 0) {  // stacked matrices: this tile's rows belong to matrix blockIdx.x / tiles_per_mat
+        const long mat = (long)blockIdx.x / tiles_per_mat;
+        uinv += mat * uinv_ms;
+        ublk += mat * ublk_ms;
+    }
     if (tid < 16) s_d[tid] = d[(row0 + tid) * ldd];
     // tile element t = 16 r + c is row r, sub-block column c
     const float g = rec[(long)blockIdx.x * 256 + tid];
@@ -163,14 +169,16 @@ extern "C" int ltq_ldlq_prep(const float* wk, long ldw, const float* d, long ldd
 extern "C" int ltq_ldlq_sub(float* wk, long ldw, const float* rec, const float* d, long ldd, const float* uinv,
                             long ldi, const float* ublk, long ldu, int ib, float* G, long ldg, float* xnext, long M,
                             const int* code, int16_t* idx, long ld_idx, uint8_t* gi, long ld_gi, float* fed,
-                            long ld_fed, void* stream)
+                            long ld_fed, long rows_per_mat, long uinv_ms, long ublk_ms, void* stream)
 {
     if (M < 0 || M % 16 || ib < 0 || ib > 15 || ldw < 256 || ldi < 256 || ldu < 256 || ldg < 256 || ldd < 1) return -1;
     if (code && (!idx || !gi || ld_idx < 256 || ld_gi < 256)) return -1;
     if (fed && ld_fed < 256) return -1;
+    if (rows_per_mat < 0 || (rows_per_mat > 0 && (rows_per_mat % 16 || M % rows_per_mat))) return -1;
     if (M == 0) return 0;
     if (!wk || !rec || !d || !uinv || !ublk || !G) return -1;
     hipLaunchKernelGGL(ldlq_sub_kernel, dim3((unsigned)(M / 16)), dim3(256), 0, (hipStream_t)stream, wk, ldw, rec, d, ldd,
-                       uinv, ldi, ublk, ldu, 16 * ib, G, ldg, xnext, M, code, idx, ld_idx, gi, ld_gi, fed, ld_fed);
+                       uinv, ldi, ublk, ldu, 16 * ib, G, ldg, xnext, M, code, idx, ld_idx, gi, ld_gi, fed, ld_fed,
+                       rows_per_mat / 16, uinv_ms, ublk_ms);
     return (int)hipGetLastError();
 }

@@ -43,6 +43,7 @@ struct GemmArgs {
     const float* b;  // B operand b[k * ldb + j], k < 256
     long ldb;
     long M, N;       // output rows, columns (N % 128 == 0)
+    long rows_per_mat, b_ms;  // stacked matrices: rows [m R, (m + 1) R) use the B operand b + m * b_ms
     // EPI 0: out[j * ld_out + i] = acc (transposed), what[i * ld_what + j] = d g (column tile 0's A values)
     // EPI 1: out[i * ld_out + j] -= acc; wsub[i * ld_wsub + j] = new value for j < 256; xnext for j < 16
     float* out;
@@ -77,6 +78,7 @@ __global__ __launch_bounds__(256) void ldlq_gemm_kernel(GemmArgs p)
     int tm, tn;
     tile_of((int)blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
     const long row0 = (long)tm * BM, col0 = (long)tn * BN;
+    if (p.rows_per_mat > 0) p.b += (row0 / p.rows_per_mat) * p.b_ms;  // a tile never straddles two matrices
     const bool write_what = EPI == 0 && p.what != nullptr && tn == 0;
 
     // staging registers of one stage: 2 float4 of A and 2 of B per thread
@@ -205,12 +207,18 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
 
+static bool bad_stack(long M, long rows_per_mat, long b_ms)
+{
+    return rows_per_mat < 0 || (rows_per_mat > 0 && (rows_per_mat % BM || M % rows_per_mat || (b_ms & 3)));
+}
+
 extern "C" int ltq_ldlq_err(const float* wstart, long ldw, const float* G, long ldg, const float* d, long ldd,
                             const float* uinv, long ldi, float* et, long ld_et, float* what, long ld_what, long M,
-                            void* stream)
+                            long rows_per_mat, long uinv_ms, void* stream)
 {
     if (M < 0 || M % 16 || ldw < 256 || ldg < 256 || ldd < 1 || ldi < 256 || ld_et < M || (what && ld_what < 256))
         return -1;
+    if (bad_stack(M, rows_per_mat, uinv_ms)) return -1;
     if (M == 0) return 0;
     if (!wstart || !G || !d || !uinv || !et) return -1;
     if ((ldw | ldg | ldi | ld_et | (what ? ld_what : 0)) & 3) return -1;
@@ -231,12 +239,16 @@ extern "C" int ltq_ldlq_err(const float* wstart, long ldw, const float* G, long 
     p.ld_out = ld_et;
     p.what = what;
     p.ld_what = ld_what;
+    p.rows_per_mat = rows_per_mat;
+    p.b_ms = uinv_ms;
     return launch_gemm(1, 0, p, (hipStream_t)stream);
 }
 
 extern "C" int ltq_ldlq_update(float* w, long ldw, const float* et, long ld_et, const float* u, long ldu, long M, long N,
-                               float* wsub, long ld_wsub, float* xnext, const float* dnext, long ld_dnext, void* stream)
+                               float* wsub, long ld_wsub, float* xnext, const float* dnext, long ld_dnext,
+                               long rows_per_mat, long u_ms, void* stream)
 {
+    if (bad_stack(M, rows_per_mat, u_ms)) return -1;
     if (M < 0 || N < 0 || M % 16 || N % BN || ldw < N || ld_et < M || ldu < N || (wsub && (ld_wsub < KD || N < KD)) ||
         (xnext && (!dnext || ld_dnext < 1 || N < 16)))
         return -1;
@@ -258,5 +270,7 @@ extern "C" int ltq_ldlq_update(float* w, long ldw, const float* et, long ld_et, 
     p.xnext = xnext;
     p.dnext = dnext;
     p.ld_dnext = ld_dnext;
+    p.rows_per_mat = rows_per_mat;
+    p.b_ms = u_ms;
     return launch_gemm(0, 1, p, (hipStream_t)stream);
 }

@@ -39,10 +39,11 @@ SIGNATURES = {
     "ltq_cov_finalize": (ci, [vp, ci, cl, cd, vp, cl, vp]),
     "ltq_row_scale": (ci, [vp, cl, cl, cl, cf, cf, ci, vp, vp, vp, cl, vp, cl, vp]),
     "ltq_ldlq_prep": (ci, [vp, cl, vp, cl, vp, cl, vp]),
-    "ltq_ldlq_sub": (ci, [vp, cl, vp, vp, cl, vp, cl, vp, cl, ci, vp, cl, vp, cl, vp, vp, cl, vp, cl, vp, cl, vp]),
+    "ltq_ldlq_sub": (ci, [vp, cl, vp, vp, cl, vp, cl, vp, cl, ci, vp, cl, vp, cl, vp, vp, cl, vp, cl, vp, cl, cl, cl, cl,
+                          vp]),
     # LDLQ block error and inter-block update on the matrix cores (src/liqk_v2.py:972-979)
-    "ltq_ldlq_err": (ci, [vp, cl, vp, cl, vp, cl, vp, cl, vp, cl, vp, cl, cl, vp]),
-    "ltq_ldlq_update": (ci, [vp, cl, vp, cl, vp, cl, cl, cl, vp, cl, vp, vp, cl, vp]),
+    "ltq_ldlq_err": (ci, [vp, cl, vp, cl, vp, cl, vp, cl, vp, cl, vp, cl, cl, cl, cl, vp]),
+    "ltq_ldlq_update": (ci, [vp, cl, vp, cl, vp, cl, cl, cl, vp, cl, vp, vp, cl, cl, cl, vp]),
 }
 
 

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import json
 from dataclasses import dataclass
+from statistics import NormalDist
 from pathlib import Path
 from typing import Dict
 
@@ -43,7 +44,24 @@ def _build_config() -> Dict[str, dict]:
                      "sub": t.get("sub", SUBBLOCK_SIZE), "pp": t.get("pp", False), "scale": xs.get(name, 1.0),
                      "m_extra": tuple(t["m_extra"]), "row_scale": True, "tb": True,
                      **({"n_cand": 4} if t["h"] > 2 else {})}
+    # the MoE expert format: K=3 D4 with 16-subset labels (the Y family's masks 40, 475), a
+    # 3-bit gain header searched over 4 candidates; no trained table exists in the reference, so its table is
+    # the closed-form start of table training (src/universal_bench.py:91-94)
+    cfg["TCQ275Y3"] = {"K": 3, "nu": 10, "m": 359, "h": 3, "step": 0.15, "lut": closed_form_lut(3, (40, 475)),
+                       "sub": SUBBLOCK_SIZE, "pp": 2, "scale": 1.1, "m_extra": (40, 475), "row_scale": True,
+                       "tb": True, "n_cand": 4}
     return cfg
+
+
+def closed_form_lut(K: int, m_extra: tuple, spread: float = 1.0) -> list:
+    """The table-training start as a list of float32 values: entry lb * U + u = the (u * nl + lb)-th of the nl * U
+    midpoint quantiles (k + 1/2) / (nl U) of N(0, spread^2), in float64 (the same values as
+    tables.closed_form_table)."""
+    nl, U = 4 << len(m_extra), 1 << (K - 1)
+    n = nl * U
+    nd = NormalDist(0.0, spread)
+    grid = np.array([nd.inv_cdf((k + 0.5) / n) for k in range(n)], dtype=np.float64).astype(np.float32)
+    return [float(grid[u * nl + lb]) for lb in range(nl) for u in range(U)]
 
 
 TCQ_CONFIG: Dict[str, dict] = _build_config()

@@ -118,12 +118,21 @@ def _quantize_rows_tcq_ldlq(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: to
     """Block16-LDLQ with every 16-column sub-block quantized in 16 x 16 tiles by the TCQ Viterbi
     (src/liqk_v2.py:877-1021, the row-scale branch; n_pass belongs to the branch without row scale and is unused).
     Returns (d_full [M, K/256] fp16, W_hat_rot [M, K]). If fed [M, K] fp32 is given, it receives the value of every
-    weight at the moment its sub-block was quantized (the Viterbi input times d).
+    weight at the moment its sub-block was quantized (the Viterbi input times d)."""
+    return _ldlq_rows(W_rot, U.unsqueeze(0), U_blks_inv.unsqueeze(0), diag_w.unsqueeze(0), spec_name, fed=fed)
 
-    Per 256-column block: 16 x (two-pass tail-biting Viterbi over the M/16 tiles, ltq_ldlq_sub: the sub-block's
+
+def _ldlq_rows(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: torch.Tensor, diag_w: torch.Tensor, spec_name: str,
+               fed: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The LDLQ loop over n stacked matrices sharing a format and a shape: W_rot [n R, K] (matrix m = rows
+    [m R, (m + 1) R)), U [n, K, K], U_blks_inv [n, K/256, 256, 256], diag_w [n, K]. Every matrix gets exactly the
+    results of its own loop; the tiles of all of them go through one Viterbi launch per sub-block.
+
+    Per 256-column block: 16 x (two-pass tail-biting Viterbi over the tiles, ltq_ldlq_sub: the sub-block's
     feedback into the block's working copy and the next tiles), then ltq_ldlq_err (the block's error E and its
     reconstruction) and ltq_ldlq_update (W[:, c1:] -= E U[c0:c1, c1:], which also writes the next block's working
-    copy and first tiles). Every sum is a fixed-order fma chain, so the loop is a defined function of its inputs."""
+    copy and first tiles). Every sum is a fixed-order fma chain, so the loop is a defined function of its inputs.
+    With PACK, appends the group's fields to PACK["groups"]."""
     cfg = TCQ_CONFIG[spec_name]
     if not cfg.get("row_scale") or "K_hi" in cfg or (cfg.get("carry") and not cfg.get("tb")):
         raise NotImplementedError(f"{spec_name}: the GPU path serves the tail-biting row-scale formats")
@@ -131,8 +140,11 @@ def _quantize_rows_tcq_ldlq(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: to
     lut = torch.tensor(cfg["lut"], dtype=torch.float32, device=device)
     gains = make_gains(cfg["h"], cfg["step"], device)
     M, K = W_rot.shape
+    n_mat = U.shape[0]
+    R = M // n_mat
     assert M % 16 == 0, "TCQ: number of rows must be divisible by 16"
-    nt = M // 16
+    assert R * n_mat == M and (n_mat == 1 or R % 128 == 0), "stacked matrices: rows per matrix a multiple of 128"
+    nt, tiles_per_mat = M // 16, R // 16
     nblocks = K // QK_K
     n_cand = int(os.environ.get("TCQ_NCAND", cfg.get("n_cand", 0)))
     tb_window = int(os.environ.get("TCQ_TB_WIN", "32"))
@@ -145,12 +157,12 @@ def _quantize_rows_tcq_ldlq(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: to
         pk = {"idx": torch.empty((M, K), dtype=torch.int16, device=device),
               "gi": torch.empty((M, K), dtype=torch.uint8, device=device),
               "G": torch.empty((M, K), dtype=torch.float32, device=device)}
-    if U.stride(1) != 1 or U.stride(0) % 4 or U.data_ptr() % 16:
-        U = U.contiguous()
-    if U_blks_inv.stride(2) != 1:
-        U_blks_inv = U_blks_inv.contiguous()
+    U = U.contiguous()
+    U_blks_inv = U_blks_inv.contiguous()
     if fed is not None:
         assert fed.shape == (M, K) and fed.dtype == torch.float32 and fed.stride(1) == 1
+    stack = (R if n_mat > 1 else 0)
+    u_ms, ubi_ms = (K * K, nblocks * QK_K * QK_K) if n_mat > 1 else (0, 0)
     d_row, e_rb, d_rb_all = row_scale(W_rot, cfg)
     d_full = d_rb_all.to(torch.float16)
     lib = _lib.lib()
@@ -164,11 +176,12 @@ def _quantize_rows_tcq_ldlq(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: to
            "ltq_ldlq_prep")
     for ibl in range(nblocks):
         c0, c1 = ibl * QK_K, (ibl + 1) * QK_K
-        U_blk = U[c0:c1, c0:c1]
-        U_blk_inv = U_blks_inv[ibl]
+        U_blk = U[0, c0:c1, c0:c1]
+        U_blk_inv = U_blks_inv[0, ibl]
         d_rb = d_rb_all[:, ibl]
-        # per-position weights of every sub-block's tiles (t = 16 r + c -> diag_w[s0 + c]), once per block
-        wts_blk = diag_w[c0:c1].view(NUM_SUBBLOCKS, 1, 1, SUBBLOCK_SIZE).expand(NUM_SUBBLOCKS, nt, 16, SUBBLOCK_SIZE)
+        # per-position weights of every sub-block's tiles (tile of matrix m, t = 16 r + c -> diag_w[m, s0 + c])
+        wts_blk = diag_w[:, c0:c1].reshape(n_mat, 1, NUM_SUBBLOCKS, 1, SUBBLOCK_SIZE)
+        wts_blk = wts_blk.expand(n_mat, tiles_per_mat, NUM_SUBBLOCKS, 16, SUBBLOCK_SIZE).permute(2, 0, 1, 3, 4)
         wts_blk = wts_blk.reshape(NUM_SUBBLOCKS, nt, 16 * SUBBLOCK_SIZE)
         G_pass, ldg = (G_buf, QK_K) if pk is None else (pk["G"][:, c0:], K)
         codes = (pk["idx"][:, c0:], pk["idx"].stride(0), pk["gi"][:, c0:], pk["gi"].stride(0)) if pk else None
@@ -181,23 +194,24 @@ def _quantize_rows_tcq_ldlq(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: to
             rec, code = out if pk is not None else (out, None)
             # G, the error feedback, the next sub-block's tiles and (PACK) the code / gain index scatter
             _check(lib.ltq_ldlq_sub(w_sub.data_ptr(), QK_K, rec.data_ptr(), d_rb.data_ptr(), nblocks,
-                                    U_blk_inv.data_ptr(), U_blk_inv.stride(0), U_blk.data_ptr(), U_blk.stride(0), ib,
+                                    U_blk_inv.data_ptr(), QK_K, U_blk.data_ptr(), K, ib,
                                     G_pass.data_ptr(), ldg, x_nxt.data_ptr() if s1 < QK_K else None, M,
                                     code.data_ptr() if code is not None else None,
                                     codes[0].data_ptr() if codes else None, codes[1] if codes else 0,
                                     codes[2].data_ptr() if codes else None, codes[3] if codes else 0,
                                     fed[:, c0:].data_ptr() if fed is not None else None,
-                                    fed.stride(0) if fed is not None else 0, stream), "ltq_ldlq_sub")
+                                    fed.stride(0) if fed is not None else 0, stack, ubi_ms, u_ms, stream),
+                   "ltq_ldlq_sub")
             x_cur, x_nxt = x_nxt, x_cur
         # the block's reconstruction and error (W_work[:, c0:c1] still holds the block's start)
-        Wb = W_work[:, c0:]
-        _check(lib.ltq_ldlq_err(Wb.data_ptr(), K, G_pass.data_ptr(), ldg, d_rb.data_ptr(), nblocks,
-                                U_blk_inv.data_ptr(), U_blk_inv.stride(0), E_t.data_ptr(), M,
-                                W_hat_rot[:, c0:].data_ptr(), K, M, stream), "ltq_ldlq_err")
+        _check(lib.ltq_ldlq_err(W_work[:, c0:].data_ptr(), K, G_pass.data_ptr(), ldg, d_rb.data_ptr(), nblocks,
+                                U_blk_inv.data_ptr(), QK_K, E_t.data_ptr(), M, W_hat_rot[:, c0:].data_ptr(), K, M,
+                                stack, ubi_ms, stream), "ltq_ldlq_err")
         if c1 < K:
-            _check(lib.ltq_ldlq_update(W_work[:, c1:].data_ptr(), K, E_t.data_ptr(), M, U[c0:c1, c1:].data_ptr(),
-                                       U.stride(0), M, K - c1, w_sub.data_ptr(), QK_K, x_cur.data_ptr(),
-                                       d_rb_all[:, ibl + 1].data_ptr(), nblocks, stream), "ltq_ldlq_update")
+            _check(lib.ltq_ldlq_update(W_work[:, c1:].data_ptr(), K, E_t.data_ptr(), M, U[0, c0:c1, c1:].data_ptr(),
+                                       K, M, K - c1, w_sub.data_ptr(), QK_K, x_cur.data_ptr(),
+                                       d_rb_all[:, ibl + 1].data_ptr(), nblocks, stack, u_ms, stream),
+                   "ltq_ldlq_update")
     if pk is not None:
         PACK["groups"].append({"spec": spec_name, "d_row": d_row, "e": e_rb, "idx": pk["idx"], "gi": pk["gi"],
                                "G": pk["G"]})

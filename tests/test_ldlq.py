@@ -155,9 +155,9 @@ def test_gpu_ldlq_err_and_update_bit_exact(oracle, M, N):
     lib, st = _lib.lib(), _lib.stream_ptr()
     print(f"ldlq err / update M={M} N={N}", flush=True)
     assert lib.ltq_ldlq_err(t["ws"].data_ptr(), 256, t["G"].data_ptr(), 256, t["d"].data_ptr(), 1, t["Ui"].data_ptr(),
-                            256, Et.data_ptr(), M, wh.data_ptr(), 256, M, st) == 0
+                            256, Et.data_ptr(), M, wh.data_ptr(), 256, M, 0, 0, st) == 0
     assert lib.ltq_ldlq_update(t["W"].data_ptr(), N, Et.data_ptr(), M, t["Up"].data_ptr(), N, M, N, wsub.data_ptr(),
-                               256, xn.data_ptr(), t["dn"].data_ptr(), 1, st) == 0
+                               256, xn.data_ptr(), t["dn"].data_ptr(), 1, 0, 0, st) == 0
     torch.cuda.synchronize()
     u32 = lambda a: np.ascontiguousarray(a).view(np.uint32)
     assert np.array_equal(u32(wh.cpu().numpy()), u32(who))
@@ -192,7 +192,7 @@ def test_gpu_ldlq_sub_bit_exact(oracle):
         rc = _lib.lib().ltq_ldlq_sub(wk_d.data_ptr(), 256, rec_d.data_ptr(), d_d.data_ptr(), 1, Ui_d.data_ptr(), 256,
                                      U_d.data_ptr(), 256, ib, G.data_ptr(), 256, xn.data_ptr(), M, code_d.data_ptr(),
                                      idx[:, 256:].data_ptr(), 512, gi[:, 256:].data_ptr(), 512, fed.data_ptr(), 256,
-                                     _lib.stream_ptr())
+                                     0, 0, 0, _lib.stream_ptr())
         assert rc == 0
         torch.cuda.synchronize()
         cv = code.view(M, 16)
