@@ -78,42 +78,98 @@ __global__ __launch_bounds__(64 * kWaves) void fwht_rows_kernel(const void* __re
     }
 }
 
-// column mode: a workgroup transforms a [256 rows, 32 columns] tile through LDS (coalesced 128-byte row
-// segments in and out); SM scales by s[row] before the transform
-constexpr int kColTile = 32;
-constexpr int kColPitch = 257;  // words per column in LDS: consecutive columns start on consecutive banks
+// column mode: a workgroup transforms a [256 rows, 64 columns] tile (64 KB of LDS, two workgroups per CU; 128
+// columns with one workgroup per CU measured 1.6x slower). Rows come in and go out as 256-byte float4 segments
+// through a row-major LDS tile; the transform runs with lane = column (every LDS access conflict-free)
+// in two register passes: stages h = 1, 2, 4, 8 over 16 consecutive rows, then h = 16, 32, 64, 128 over 16 rows
+// spaced 16 apart (the same stage order and pairs as the reference, so the same bits). SM scales by s[row]
+// before the transform.
+constexpr int kColTile = 64;
 
 template <int SM>
 __global__ __launch_bounds__(64 * kWaves) void fwht_cols_kernel(const float* __restrict__ x, float* __restrict__ y,
                                                                long rows, long cols, long ldx, long ldy,
-                                                               const float* __restrict__ s)
+                                                               const float* __restrict__ s, int vec)
 {
-    __shared__ float t[kColTile * kColPitch];
+    __shared__ __align__(16) float t[256][kColTile];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const long ctiles = (cols + kColTile - 1) / kColTile;
     const long total = (rows / 256) * ctiles;
+    const int c4 = 4 * (tid & 15), i0 = tid >> 4;  // rows i0 + 16 k, columns c4 .. c4 + 3
     for (long u = blockIdx.x; u < total; u += gridDim.x) {
-        const long r0 = (u / ctiles) * 256, c0 = (u % ctiles) * kColTile;
-        const int cc = tid & (kColTile - 1);
-        const bool in = c0 + cc < cols;
-        for (int i = tid / kColTile; i < 256; i += 64 * kWaves / kColTile) {
-            float v = in ? x[(r0 + i) * ldx + c0 + cc] : 0.f;
-            if constexpr (SM == 1) v = v / s[r0 + i];
-            else if constexpr (SM == 2) v = v * s[r0 + i];
-            t[cc * kColPitch + i] = v;
+        const long r0 = (u / ctiles) * 256, cg = (u % ctiles) * kColTile + c4;
+        for (int k = 0; k < 16; k++) {
+            const long row = r0 + i0 + 16 * k;
+            float4 f;
+            if (vec && cg + 3 < cols) {
+                f = *(const float4*)(x + row * ldx + cg);
+            } else {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = cg + e < cols ? x[row * ldx + cg + e] : 0.f;
+                f = make_float4(v[0], v[1], v[2], v[3]);
+            }
+            if constexpr (SM != 0) {
+                const float sr = s[row];
+                if constexpr (SM == 1) {
+                    f.x = f.x / sr; f.y = f.y / sr; f.z = f.z / sr; f.w = f.w / sr;
+                } else {
+                    f.x = f.x * sr; f.y = f.y * sr; f.z = f.z * sr; f.w = f.w * sr;
+                }
+            }
+            *(float4*)&t[i0 + 16 * k][c4] = f;
         }
         __syncthreads();
-        for (int c = wv; c < kColTile; c += kWaves) {
-            float v[4];
+        // pass 1: wave w, row groups 4 w .. 4 w + 3 of 16 consecutive rows; stages h = 1, 2, 4, 8
+        for (int gq = 0; gq < 4; gq++) {
+            const int rb = 16 * (4 * wv + gq);
+            float v[16];
 #pragma unroll
-            for (int i = 0; i < 4; i++) v[i] = t[c * kColPitch + 4 * lane + i];
-            fwht_wave(v, lane);
+            for (int k = 0; k < 16; k++) v[k] = t[rb + k][lane];
 #pragma unroll
-            for (int i = 0; i < 4; i++) t[c * kColPitch + 4 * lane + i] = v[i];
+            for (int h = 1; h < 16; h <<= 1)
+#pragma unroll
+                for (int k = 0; k < 16; k++)
+                    if (!(k & h)) {
+                        const float a = v[k], b = v[k + h];
+                        v[k] = a + b;
+                        v[k + h] = a - b;
+                    }
+#pragma unroll
+            for (int k = 0; k < 16; k++) t[rb + k][lane] = v[k];
         }
         __syncthreads();
-        if (in)
-            for (int i = tid / kColTile; i < 256; i += 64 * kWaves / kColTile) y[(r0 + i) * ldy + c0 + cc] = t[cc * kColPitch + i];
+        // pass 2: wave w, rows r_lo + 16 k for r_lo = 4 w .. 4 w + 3; stages h = 16 .. 128, then x 0.0625
+        for (int gq = 0; gq < 4; gq++) {
+            const int rl = 4 * wv + gq;
+            float v[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = t[rl + 16 * k][lane];
+#pragma unroll
+            for (int h = 1; h < 16; h <<= 1)
+#pragma unroll
+                for (int k = 0; k < 16; k++)
+                    if (!(k & h)) {
+                        const float a = v[k], b = v[k + h];
+                        v[k] = a + b;
+                        v[k + h] = a - b;
+                    }
+#pragma unroll
+            for (int k = 0; k < 16; k++) t[rl + 16 * k][lane] = v[k] * 0.0625f;
+        }
+        __syncthreads();
+        for (int k = 0; k < 16; k++) {
+            const long row = r0 + i0 + 16 * k;
+            const float4 f = *(const float4*)&t[i0 + 16 * k][c4];
+            if (vec && cg + 3 < cols) {
+                *(float4*)(y + row * ldy + cg) = f;
+            } else {
+                const float v[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (cg + e < cols) y[row * ldy + cg + e] = v[e];
+            }
+        }
         __syncthreads();
     }
 }
@@ -171,11 +227,12 @@ extern "C" int ltq_fwht256_cols(const float* x, float* y, long rows, long cols, 
     if (!x || !y || ((uintptr_t)s & 3)) return -1;  // in place is fine: a tile is read whole before it is written
     hipStream_t st = (hipStream_t)stream;
     const long tiles = (rows / 256) * ((cols + kColTile - 1) / kColTile);
-    int grid = grid_for(tiles * kWaves);
+    const int grid = grid_for(tiles * kWaves);
+    const int vec = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && ldx % 4 == 0 && ldy % 4 == 0;
     switch (smode) {
-        case 0: hipLaunchKernelGGL((fwht_cols_kernel<0>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s); break;
-        case 1: hipLaunchKernelGGL((fwht_cols_kernel<1>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s); break;
-        default: hipLaunchKernelGGL((fwht_cols_kernel<2>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s); break;
+        case 0: hipLaunchKernelGGL((fwht_cols_kernel<0>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s, vec); break;
+        case 1: hipLaunchKernelGGL((fwht_cols_kernel<1>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s, vec); break;
+        default: hipLaunchKernelGGL((fwht_cols_kernel<2>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s, vec); break;
     }
     return (int)hipGetLastError();
 }

@@ -47,14 +47,26 @@ __global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict_
     float* rms = s_rms + wv * nblk;
     const float* wr = w + row * ldw;
     double lsum = 0.0;
-    for (int b = 0; b < nblk; b++) {
-        const float4 v = *(const float4*)(wr + b * 256 + 4 * lane);
-        float s = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    constexpr int kAhead = 8;  // blocks whose loads are in flight together
+    for (int b0 = 0; b0 < nblk; b0 += kAhead) {
+        float4 v[kAhead];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-        const float r = fmaxf(sqrtf(s / 256.f), 1e-10f) * scale;
-        if (lane == 0) rms[b] = r;
-        lsum += log((double)r);  // every lane holds the same r
+        for (int j = 0; j < kAhead; j++)
+            if (b0 + j < nblk) v[j] = *(const float4*)(wr + (b0 + j) * 256 + 4 * lane);
+        float s[kAhead];
+#pragma unroll
+        for (int j = 0; j < kAhead; j++) s[j] = v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+            for (int j = 0; j < kAhead; j++) s[j] += __shfl_xor(s[j], o, 64);
+#pragma unroll
+        for (int j = 0; j < kAhead; j++) {
+            if (b0 + j >= nblk) break;
+            const float r = fmaxf(sqrtf(s[j] / 256.f), 1e-10f) * scale;
+            if (lane == 0) rms[b0 + j] = r;
+            lsum += log((double)r);  // every lane holds the same r; blocks summed in order
+        }
     }
     const float d = fmaxf(__half2float(__float2half((float)exp(lsum / (double)nblk))), 1e-8f);
     if (lane == 0) d_row[row] = d;

@@ -7,8 +7,8 @@
 //   lsb    [T, 16 | 8 | 12]     lowest uncoded bit: every position / one per pair (D2) / three per quad (D4)
 //   gains  [T, ceil(256/sub*h/16)] u16   gain index of each sub-block, h bits LSB first, back to back
 // Tiles are ordered by row group then 16-column block; tile position t = 16 r + c is row 16 rg + r, column
-// 16 kb + c. One wavefront packs one tile: it stages the tile's 256 codes in LDS, then each lane assembles
-// whole 16-bit words.
+// 16 kb + c. A workgroup packs a strip of 16 consecutive tiles of one row group: contiguous row loads into LDS,
+// every 64 bits of a field's stream from one wavefront ballot, each region's run of the strip written at once.
 //
 // Row rings (src/ltq_format.py:42-50, 104-124 with L instead of 256; the ring tables of src/ple_quant.py): a
 // ring of L positions (L % 16 == 0, L <= 512) packs into one record of the same four fields back to back,
@@ -87,36 +87,48 @@ __device__ inline void wave_sync()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Word wr of field reg of one tile / ring whose codes and gain indices sit in LDS (position t = 0 .. L-1):
-//   codes  bit j of word w = label & 1 at position 16 w + j
-//   planes plane p = 1 .. K-2 of u, L/16 words each, same layout
-//   lsb    lowest bit of u: every position / one per pair (D2) / the first three of each quad (D4)
-//   gains  gain index of each sub-block, h bits LSB first, back to back
-__device__ inline uint32_t field_word(const int16_t* ix, const uint8_t* gs, const PackGeo& g, int reg, int wr)
+// Bit streams of the four fields of one tile / ring of L positions, as wave ballots: the bit of stream element
+// e = 64 q + lane is computed by lane `lane`, ballot(bit) is 64 consecutive stream bits = 4 consecutive u16
+// words, and lanes 0..3 hand one word each to store(field, word, value).
+//   codes   e = position t:                       bit K-1 of the code (= label & 1)
+//   planes  e = position t, plane p = 1 .. K-2:   bit p of u (= code & (U - 1))
+//   lsb     frac 0: e = t; 1 (D2): t = 2 e; 2 (D4): t = 4 (e / 3) + e % 3 (the first three of each quad): bit 0
+//   gains   e < (L / sub) h: bit e % h of the gain index at the first position of sub-block e / h
+// ixat(t) / gat(t) read the code / gain index of position t; bits past a stream's end are 0.
+template <class IX, class GG, class ST>
+__device__ inline void ballot_fields(const PackGeo& g, int lane, IX ixat, GG gat, ST store)
 {
-    const int W = g.L / 16;
-    uint32_t word = 0;
-    for (int j = 0; j < 16; j++) {
-        const int i = 16 * wr + j;  // bit index within the field's stream
-        uint32_t bit = 0;
-        if (reg == 0) {
-            bit = ((uint32_t)ix[i] >> (g.K - 1)) & 1;
-        } else if (reg == 1) {
-            const int p = 1 + wr / W, t = 16 * (wr % W) + j;
-            bit = (((uint32_t)ix[t] & (g.U - 1)) >> p) & 1;
-        } else if (reg == 2) {
-            if (i < lsb_bits(g.frac, g.L)) {
-                const int t = g.frac == 0 ? i : g.frac == 1 ? 2 * i : 4 * (i / 3) + i % 3;
-                bit = (uint32_t)ix[t] & 1;
-            }
-        } else {
-            if (i < g.L / g.sub * g.h) bit = ((uint32_t)gs[g.sub * (i / g.h)] >> (i % g.h)) & 1;
-        }
-        word |= bit << j;
+    const int L = g.L, W = L / 16;
+    auto put = [&](int field, int w0, int nw, unsigned long long m) {
+        if (lane < 4 && w0 + lane < nw) store(field, w0 + lane, (uint16_t)(m >> (16 * lane)));
+    };
+    for (int q = 0; q < (L + 63) / 64; q++) {
+        const int t = 64 * q + lane;
+        const uint32_t v = t < L ? (uint32_t)(uint16_t)ixat(t) : 0u;
+        put(0, 4 * q, W, __ballot((v >> (g.K - 1)) & 1u));
+        for (int p = 1; p < g.K - 1; p++) put(1, (p - 1) * W + 4 * q, p * W, __ballot(((v & (g.U - 1)) >> p) & 1u));
+        if (g.K > 1 && g.frac == 0) put(2, 4 * q, W, __ballot(v & 1u));
     }
-    return word;
+    if (g.K > 1 && g.frac != 0) {
+        const int nb = lsb_bits(g.frac, L);
+        for (int q = 0; q < (nb + 63) / 64; q++) {
+            const int e = 64 * q + lane;
+            const int t = g.frac == 1 ? 2 * e : 4 * (e / 3) + e % 3;
+            const uint32_t b = e < nb ? ((uint32_t)(uint16_t)ixat(t) & 1u) : 0u;
+            put(2, 4 * q, g.n[2], __ballot(b));
+        }
+    }
+    if (g.h) {
+        const int nb = L / g.sub * g.h;
+        for (int q = 0; q < (nb + 63) / 64; q++) {
+            const int e = 64 * q + lane;
+            const uint32_t b = e < nb ? ((uint32_t)gat(g.sub * (e / g.h)) >> (e % g.h)) & 1u : 0u;
+            put(3, 4 * q, g.n[3], __ballot(b));
+        }
+    }
 }
 
+// field and word within it of word w of a tile / ring's concatenated fields
 __device__ inline void word_region(const PackGeo& g, int w, int& reg, int& wr)
 {
     reg = 0;
@@ -127,41 +139,73 @@ __device__ inline void word_region(const PackGeo& g, int w, int& reg, int& wr)
     }
 }
 
-__global__ __launch_bounds__(64 * kWaves) void pack_kernel(const int16_t* __restrict__ idx, long ld_idx,
-                                                           const uint8_t* __restrict__ gi, long ld_gi, int R, int Kc,
-                                                           PackGeo g, uint8_t* __restrict__ out)
+constexpr int kStrip = 16;             // tiles per workgroup: one row group, 16 consecutive 16-column blocks
+constexpr int kMaxTileWords = 256;     // codes 16 + planes 16 (K-2) <= 96 + lsb <= 16 + gains 256 / sub h / 16 <= 128
+
+// One workgroup (4 wavefronts) per strip of 16 consecutive tiles of one row group: the strip's 16 rows x 256
+// columns of codes and gain indices come in as contiguous 16-byte row loads into LDS, each wavefront turns tiles
+// j = wave, wave + 4, ... into their words (ballot_fields) staged field by field, and each field's words of the
+// strip -- contiguous in the output, tiles being consecutive -- are written as one run of u16 stores. (A
+// wavefront per 4 tiles without workgroup barriers, or per whole strip, measured slower: 137 and 246 us
+// against 128 us for the C3 slice.) Dynamic LDS: the staging, 16 x tile words x 2 bytes.
+__global__ __launch_bounds__(256) void pack_strip_kernel(const int16_t* __restrict__ idx, long ld_idx,
+                                                         const uint8_t* __restrict__ gi, long ld_gi, int R, int Kc,
+                                                         PackGeo g, int vec, uint8_t* __restrict__ out)
 {
-    __shared__ int16_t s_ix[kWaves][256];
-    __shared__ uint8_t s_g[kWaves][256];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int kbs = Kc / 16;
+    __shared__ __align__(16) int16_t s_ix[16][kStrip * 16];
+    __shared__ __align__(16) uint8_t s_g[16][kStrip * 16];
+    extern __shared__ uint16_t s_w[];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int kbs = Kc / 16, spr = (kbs + kStrip - 1) / kStrip;
     const long T = (long)(R / 16) * kbs;
     // zero the gaps between regions (the reference pads with zero bytes)
     if (blockIdx.x == 0) {
         for (int r = 1; r < 4; r++) {
             const long end_prev = g.off[r - 1] + 2 * T * g.n[r - 1];
-            for (long b = end_prev + threadIdx.x; b < g.off[r]; b += blockDim.x) out[b] = 0;
+            for (long b = end_prev + tid; b < g.off[r]; b += blockDim.x) out[b] = 0;
         }
     }
-    for (long tile = (long)blockIdx.x * kWaves + wv; tile < T; tile += (long)gridDim.x * kWaves) {
-        const long rg = tile / kbs, kb = tile - rg * kbs;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = 4 * lane + i, r = t >> 4, c = t & 15;
-            const long row = rg * 16 + r, col = kb * 16 + c;
-            s_ix[wv][t] = idx[row * ld_idx + col];
-            s_g[wv][t] = gi[row * ld_gi + col];
+    const long rg = (long)blockIdx.x / spr;
+    const int kb0 = (int)((long)blockIdx.x % spr) * kStrip;
+    const int nt = kbs - kb0 < kStrip ? kbs - kb0 : kStrip;
+    {  // thread (row r, chunk c) loads the strip's columns 16 c .. 16 c + 15 of row r
+        const int r = tid >> 4, c = tid & 15;
+        if (c < nt) {
+            const long row = rg * 16 + r, col = (long)(kb0 + c) * 16;
+            const int16_t* src = idx + row * ld_idx + col;
+            const uint8_t* gsrc = gi + row * ld_gi + col;
+            if (vec) {
+                *(uint4*)&s_ix[r][16 * c] = *(const uint4*)src;
+                *(uint4*)&s_ix[r][16 * c + 8] = *(const uint4*)(src + 8);
+                *(uint4*)&s_g[r][16 * c] = *(const uint4*)gsrc;
+            } else {
+                for (int k = 0; k < 16; k++) {
+                    s_ix[r][16 * c + k] = src[k];
+                    s_g[r][16 * c + k] = gsrc[k];
+                }
+            }
         }
-        wave_sync();
-        const int W = g.n[0] + g.n[1] + g.n[2] + g.n[3];
-        for (int w = lane; w < W; w += 64) {
-            int reg, wr;
-            word_region(g, w, reg, wr);
-            *(uint16_t*)(out + g.off[reg] + 2 * (tile * g.n[reg] + wr)) = (uint16_t)field_word(s_ix[wv], s_g[wv], g, reg, wr);
-        }
-        wave_sync();
+    }
+    __syncthreads();
+    int base[4];
+    base[0] = 0;
+    for (int f = 1; f < 4; f++) base[f] = base[f - 1] + kStrip * g.n[f - 1];
+    for (int j = wv; j < nt; j += 4) {
+        ballot_fields(
+            g, lane, [&](int t) { return s_ix[t >> 4][16 * j + (t & 15)]; },
+            [&](int t) { return s_g[t >> 4][16 * j + (t & 15)]; },
+            [&](int f, int w, uint16_t v) { s_w[base[f] + j * g.n[f] + w] = v; });
+    }
+    __syncthreads();
+    const long T0 = rg * kbs + kb0;
+    for (int f = 0; f < 4; f++) {
+        uint16_t* dst = (uint16_t*)(out + g.off[f]) + T0 * g.n[f];
+        const int cnt = nt * g.n[f];
+        for (int w = tid; w < cnt; w += 256) dst[w] = s_w[base[f] + w];
     }
 }
+
+constexpr int kMaxRingWords = 512;  // codes 32 + planes <= 192 + lsb 32 + gains <= 256 for L <= 512
 
 // one wavefront per ring: record i = fields codes, planes, lsb, gains back to back (g.total bytes)
 __global__ __launch_bounds__(64 * kWaves) void pack_rings_kernel(const int16_t* __restrict__ idx, long ld_idx,
@@ -170,6 +214,7 @@ __global__ __launch_bounds__(64 * kWaves) void pack_rings_kernel(const int16_t* 
 {
     __shared__ int16_t s_ix[kWaves][kMaxL];
     __shared__ uint8_t s_g[kWaves][kMaxL];
+    __shared__ uint16_t s_w[kWaves][kMaxRingWords];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int W = g.n[0] + g.n[1] + g.n[2] + g.n[3];
     for (long ring = (long)blockIdx.x * kWaves + wv; ring < n; ring += (long)gridDim.x * kWaves) {
@@ -178,12 +223,12 @@ __global__ __launch_bounds__(64 * kWaves) void pack_rings_kernel(const int16_t* 
             s_g[wv][t] = gi[ring * ld_gi + t];
         }
         wave_sync();
+        ballot_fields(
+            g, lane, [&](int t) { return s_ix[wv][t]; }, [&](int t) { return s_g[wv][t]; },
+            [&](int f, int w, uint16_t v) { s_w[wv][g.off[f] + w] = v; });
+        wave_sync();
         uint16_t* rec = (uint16_t*)(out + ring * g.total);
-        for (int w = lane; w < W; w += 64) {
-            int reg, wr;
-            word_region(g, w, reg, wr);
-            rec[g.off[reg] + wr] = (uint16_t)field_word(s_ix[wv], s_g[wv], g, reg, wr);
-        }
+        for (int w = lane; w < W; w += 64) rec[w] = s_w[wv][w];
         wave_sync();
     }
 }
@@ -209,11 +254,14 @@ extern "C" int ltq_pack_slice(const int16_t* idx, long ld_idx, const uint8_t* gi
     if (R == 0 || K == 0) return 0;
     if (!idx || !gi || !out) return -1;
     const PackGeo g = pack_geo(R, K, fmt_K, frac, h, sub);
-    const long T = (long)(R / 16) * (K / 16);
-    long grid = (T + kWaves - 1) / kWaves;
-    if (grid > 65536) grid = 65536;
-    hipLaunchKernelGGL(pack_kernel, dim3((unsigned)grid), dim3(64 * kWaves), 0, (hipStream_t)stream, idx, ld_idx, gi, ld_gi,
-                       R, K, g, out);
+    if (g.n[0] + g.n[1] + g.n[2] + g.n[3] > kMaxTileWords) return -1;
+    const long kbs = K / 16, spr = (kbs + kStrip - 1) / kStrip;
+    const long grid = (long)(R / 16) * spr;
+    if (grid > 0x7fffffffL) return -1;
+    const int vec = ((uintptr_t)idx % 16 == 0) && ((uintptr_t)gi % 16 == 0) && ld_idx % 8 == 0 && ld_gi % 16 == 0;
+    const size_t stage = (size_t)kStrip * (g.n[0] + g.n[1] + g.n[2] + g.n[3]) * sizeof(uint16_t);  // <= 8 KB
+    hipLaunchKernelGGL(pack_strip_kernel, dim3((unsigned)grid), dim3(256), stage, (hipStream_t)stream, idx, ld_idx, gi,
+                       ld_gi, R, K, g, vec, out);
     return (int)hipGetLastError();
 }
 
@@ -231,6 +279,7 @@ extern "C" int ltq_pack_rings(const int16_t* idx, long ld_idx, const uint8_t* gi
     if (n_rings == 0) return 0;
     if (!idx || !gi || !out) return -1;
     const PackGeo g = ring_geo(L, fmt_K, frac, h, sub);
+    if (g.n[0] + g.n[1] + g.n[2] + g.n[3] > kMaxRingWords) return -1;
     long grid = (n_rings + kWaves - 1) / kWaves;
     if (grid > 65536) grid = 65536;
     hipLaunchKernelGGL(pack_rings_kernel, dim3((unsigned)grid), dim3(64 * kWaves), 0, (hipStream_t)stream, idx, ld_idx, gi,
