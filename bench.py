@@ -13,8 +13,10 @@ feedback, then the c_row / suh refit.
 
 Prints one JSON line (driver contract). `roofline` is the dominant kernel (the Viterbi) against the gfx950
 fp32 VALU peak, from HIP events recorded around every Viterbi pass of one sub-block in 16 inside the timed
-region, on the stream the kernels run on; `cpu_baseline` is the C oracle (a scalar-per-thread port of the
-reference semantics, OpenMP over tiles) timed on this host on a bounded sample of the same workload.
+region, on the stream the kernels run on; `cpu_baseline` is the reference's CPU path -- torch, eager, every core
+of this host (oracle/torch_viterbi.py restates viterbi_ub with the production semantics, pinned to the
+reference's outputs) plus the LDLQ feedback -- on the first sub-blocks of the same matrix, extrapolated to the
+whole matrix; `cpu_baseline_c_port` is the C oracle on the same tiles (Viterbi stage only).
 """
 from __future__ import annotations
 
@@ -87,21 +89,101 @@ def build_hessian(X):
                "kernel": "ltq_cov_accumulate (cov_kernel<bf16>), fp32 MFMA accumulation into fp64 H"}
 
 
-def sample_tiles(W, H, nsub):
-    """Viterbi tiles and weights of the first nsub sub-blocks (block 0, no LDLQ feedback yet applied beyond the
-    first sub-block) for the CPU baseline: rotation, row scale and factors as the GPU step computes them."""
-    import torch
+def block_inputs(W, H):
+    """W_rot, U, U_blks_inv[0], diag_w and the block scales of the first 256-column block, computed by the product
+    path (rotation, factors, row scale) and copied to the host: the inputs of the CPU baselines."""
     from ltq_amd import liqk, rotation
     from ltq_amd.formats import TCQ_CONFIG
     cfg = TCQ_CONFIG[FORMAT]
     W_rot, H_rot, _ = rotation.compute_optimal_suh(W.float(), H.float(), seed=1337)
-    _, diag_w, _ = liqk.factor_hessian(H_rot, DAMP)
+    U, diag_w, Ub_inv = liqk.factor_hessian(H_rot, DAMP)
     _, _, d = liqk.row_scale(W_rot, cfg)
-    rows = W.shape[0]
-    xs = W_rot[:, :256].view(rows, 16, 16) / d[:, 0].view(rows, 1, 1)
-    tiles = xs.view(rows // 16, 16, 16, 16).permute(2, 0, 1, 3).contiguous().view(16, rows // 16, 256)
-    wts = diag_w[:256].view(16, 16).repeat(1, 16).contiguous()
-    return tiles[:nsub].cpu(), wts[:nsub].cpu()
+    return (W_rot[:, :256].cpu(), U[:256, :256].cpu(), Ub_inv[0].cpu(), diag_w[:256].cpu(), d[:, 0].cpu())
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_torch(inputs, budget_s, total_subblocks):
+    """BASELINE.md's CPU baseline: the reference's CPU path -- torch on the host, eager, every available core --
+    over the first 256-column block of the same matrix with its LDLQ feedback (src/liqk_v2.py:948-970: torch
+    matmuls), the Viterbi by oracle/torch_viterbi.py (the torch restatement of viterbi_ub with the kernel's D4 /
+    tail-biting semantics). Sub-blocks run in order until budget_s is spent (at least one); the whole-matrix rate
+    is extrapolated from them."""
+    import numpy as np
+    import torch
+    from oracle import torch_viterbi
+    from ltq_amd.formats import TCQ_CONFIG, make_format
+    cfg, f = TCQ_CONFIG[FORMAT], make_format(FORMAT)
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    W_rot, U_blk, U_inv, diag_w, d = (t.float() for t in inputs)
+    rows = W_rot.shape[0]
+    w_sub = W_rot.clone()
+    inv_d = 1.0 / d.clamp(min=1e-8).unsqueeze(1)
+    done, t0 = 0, time.perf_counter()
+    for ib in range(16):
+        s0, s1 = 16 * ib, 16 * ib + 16
+        x = (w_sub[:, s0:s1] * inv_d).contiguous().view(rows // 16, 256).numpy()
+        rec, _, _ = torch_viterbi.viterbi_ub_cuda_torch(x, f.lut, f.K, 10, 359, f.gain_tab, sub=16,
+                                                        wts=np.tile(diag_w[s0:s1].numpy(), 16),
+                                                        n_cand=cfg.get("n_cand", 0), tail_biting=True,
+                                                        tb_window=TB_WINDOW, m_extra=f.masks[1:],
+                                                        pair_parity=int(cfg["pp"]))
+        g_sub = torch.from_numpy(rec).view(rows, 16)
+        if s1 < 256:
+            err = (w_sub[:, s0:s1] - d.unsqueeze(1) * g_sub) @ U_inv[s0:s1, s0:s1]
+            w_sub[:, s1:] -= err @ U_blk[s0:s1, s1:]
+        done += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    per_sub = dt / done
+    total = per_sub * total_subblocks
+    weights = rows * 16 * total_subblocks
+    return {"value": round(weights / total / 1e6, 5), "unit": "Mweights/s", "cores": cores, "kind": "port",
+            "extrapolated": True, "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
+            "sample": f"torch (eager, {cores} threads) restatement of the reference's CPU Viterbi "
+                      f"(oracle/torch_viterbi.py, src/tcq_proto.py:327-419 with the kernel's D4 / tail-biting "
+                      f"semantics) plus the LDLQ sub-block feedback in torch, over the first {done} sub-blocks of "
+                      f"the first 256-column block ({rows} x {16 * done} weights) in {dt:.1f} s; whole matrix "
+                      f"extrapolated x{total_subblocks / done:.0f} ({per_sub:.2f} s per sub-block)"}
+
+
+def cpu_baseline_port(inputs, budget_s):
+    """The C oracle (oracle/ltq_oracle.c, OpenMP over tiles) on the same sub-blocks: Viterbi stage only."""
+    import numpy as np
+    from oracle import ref
+    from ltq_amd.formats import TCQ_CONFIG, make_format
+    f = make_format(FORMAT)
+    cfg = TCQ_CONFIG[FORMAT]
+    W_rot, _, _, diag_w, d = inputs
+    rows = W_rot.shape[0]
+    cores = min(16, len(os.sched_getaffinity(0)))
+    ref.lib()
+    xs = (W_rot.float() / d.clamp(min=1e-8).unsqueeze(1)).view(rows // 16, 16, 16, 16).permute(2, 0, 1, 3)
+    xs = xs.contiguous().view(16, rows // 16, 256)
+    done, nsub, t0 = 0, 0, time.perf_counter()
+    while time.perf_counter() - t0 <= budget_s:
+        s = nsub % 16
+        ref.viterbi_ub_cuda_ref(xs[s].numpy(), f.lut, f.K, 10, 359, f.gain_tab, sub=f.sub,
+                                wts=np.tile(diag_w[16 * s:16 * s + 16].numpy(), 16), n_cand=cfg.get("n_cand", 0),
+                                tail_biting=True, tb_window=TB_WINDOW, m_extra=f.masks[1:],
+                                pair_parity=int(cfg["pp"]), return_code=True, nthreads=cores)
+        done += xs.shape[1] * 256
+        nsub += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(done / dt / 1e6, 4), "unit": "Mweights/s", "cores": cores, "kind": "port",
+            "sample": f"oracle/ltq_oracle.c two-pass tail-biting Viterbi (a C port, OpenMP over tiles), {nsub} "
+                      f"sub-block launches over the first block's sub-blocks ({done} weights) in {dt:.1f} s on "
+                      f"{cores} threads; the Viterbi stage only, to compare with breakdown.mweights_s_viterbi"}
 
 
 def lane_ops_per_launch(cfg, tiles, steps):
@@ -211,34 +293,6 @@ class KernelTimer:
                 d["frac_mfma_fp32"] = round(fl / t / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4)
             out[name] = d
         return out
-
-
-def cpu_baseline(tiles, wts, budget_s):
-    """The C oracle (OpenMP over tiles) on the first sub-blocks, in quantization order, until budget_s is spent."""
-    import numpy as np
-    from oracle import ref
-    from ltq_amd.formats import make_format, TCQ_CONFIG
-    f = make_format(FORMAT)
-    cfg = TCQ_CONFIG[FORMAT]
-    cores = min(16, len(os.sched_getaffinity(0)))
-    ref.lib()
-    done, t0 = 0, time.perf_counter()
-    nsub = 0
-    while time.perf_counter() - t0 <= budget_s:  # cycles through the sample's sub-blocks until the budget is spent
-        s = nsub % tiles.shape[0]
-        x = tiles[s].numpy()
-        w = wts[s].numpy()
-        ref.viterbi_ub_cuda_ref(x, f.lut, f.K, 10, 359, f.gain_tab, sub=f.sub, wts=w, n_cand=cfg.get("n_cand", 0),
-                                tail_biting=True, tb_window=TB_WINDOW, m_extra=f.masks[1:], pair_parity=int(cfg["pp"]),
-                                return_code=True, nthreads=cores)
-        done += x.size
-        nsub += 1
-    dt = time.perf_counter() - t0
-    return {"value": round(done / dt / 1e6, 4), "unit": "Mweights/s", "cores": cores, "kind": "port",
-            "sample": f"oracle/ltq_oracle.c two-pass tail-biting Viterbi, {nsub} sub-block launches cycling over the "
-                      f"first {tiles.shape[0]} sub-blocks of block 0 "
-                      f"({nsub} x {tiles.shape[1]} tiles x 256 weights = {done} weights) in {dt:.1f} s on {cores} threads; "
-                      f"the Viterbi stage only, to compare with breakdown.mweights_s_viterbi"}
 
 
 C5_ROWS, C5_COLS = 262144, 2560  # BASELINE.json configs[4]: K=4 D4 rings = TCQ375X; TCQ4X on request
@@ -573,9 +627,9 @@ def main():
         "ldlq_update": kernels.get("ldlq_update"),
     }
     if args.cpu_seconds > 0:
-        nsub = 16
-        tiles, wts = sample_tiles(W, H, nsub)
-        out["cpu_baseline"] = cpu_baseline(tiles, wts, args.cpu_seconds)
+        inputs = block_inputs(W, H)
+        out["cpu_baseline"] = cpu_baseline_torch(inputs, args.cpu_seconds, (cols // 256) * 16)
+        out["cpu_baseline_c_port"] = cpu_baseline_port(inputs, min(args.cpu_seconds, 10.0))
     print(json.dumps(out), flush=True)
 
 
