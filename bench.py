@@ -191,6 +191,19 @@ def lane_ops_per_launch(cfg, tiles, steps):
     return tiles * steps * LANE_OPS_PER_STEP[int(cfg.get("pp", 0))] * 1024 * G
 
 
+def viterbi_event_totals(records):
+    """(seconds, lane-ops, launches) summed over tcq_proto timing-hook records: each record is one event pair
+    around one Viterbi call (both passes of a tail-biting call) with the (steps, gain slots) of every launch."""
+    secs = ops = 0.0
+    n = 0
+    for r in records:
+        secs += r["ev"][0].elapsed_time(r["ev"][1]) * 1e-3
+        for steps, G in r["launches"]:
+            ops += r["tiles"] * steps * LANE_OPS_PER_STEP[r["pp"]] * 1024 * G
+            n += 1
+    return secs, ops, n
+
+
 def read_traffic():
     """HBM bytes per Viterbi launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (committed summary)."""
     p = ROOT / "profiles" / "tcq_viterbi_c3_tcq275x2_traffic.txt"
@@ -204,6 +217,66 @@ def read_traffic():
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 MFMA_FP32_PEAK_TFLOPS = 157.3
+
+
+class DeviceEvent:
+    """A HIP timing event (hipEventCreateWithFlags, hipEventDisableSystemFence: an event only used to measure
+    time). record(stream) enqueues it as a marker, as torch.cuda.Event does; `handle` (the hipEvent_t) lets
+    tcq_proto hand it to the Viterbi launches themselves (ltq_viterbi_timing -> hipExtLaunchKernelGGL), which
+    stamp it with the dispatch's own start / end time. A marker between two kernels costs about 5 us of idle
+    dispatch gap on each side on MI355X (measured against the kernel trace), time the kernel does not spend.
+    elapsed_time(end) in ms."""
+    _hip = None
+
+    @classmethod
+    def _runtime(cls):
+        if cls._hip is None:
+            import ctypes
+            import torch
+            torch.cuda.init()
+            path = next((ln.split()[-1] for ln in open("/proc/self/maps") if "libamdhip64.so" in ln), "libamdhip64.so")
+            h = ctypes.CDLL(path)
+            h.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+            h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+            h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+            h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+            for f in ("hipEventCreateWithFlags", "hipEventRecord", "hipEventSynchronize", "hipEventElapsedTime",
+                      "hipEventDestroy"):
+                getattr(h, f).restype = ctypes.c_int
+            cls._hip = h
+        return cls._hip
+
+    def __init__(self):
+        import ctypes
+        self._ev = ctypes.c_void_p()
+        rc = self._runtime().hipEventCreateWithFlags(ctypes.byref(self._ev), 0x20000000)  # DisableSystemFence
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags: HIP error {rc}")
+
+    @property
+    def handle(self):
+        return self._ev.value
+
+    def record(self, stream=None):
+        import torch
+        st = stream if stream is not None else torch.cuda.current_stream()
+        rc = self._hip.hipEventRecord(self._ev, st.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord: HIP error {rc}")
+
+    def elapsed_time(self, end):
+        import ctypes
+        ms = ctypes.c_float()
+        if self._hip.hipEventSynchronize(end._ev) != 0 or self._hip.hipEventElapsedTime(ctypes.byref(ms), self._ev,
+                                                                                         end._ev) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def __del__(self):
+        if self._ev and self._hip is not None:
+            self._hip.hipEventDestroy(self._ev)
+            self._ev = None
 
 
 class KernelTimer:
@@ -223,7 +296,7 @@ class KernelTimer:
             if not self.active:
                 return orig(*a, **k)
             st = torch.cuda.current_stream()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0, e1 = DeviceEvent(), DeviceEvent()
             e0.record(st)
             out = orig(*a, **k)
             e1.record(st)
@@ -346,18 +419,18 @@ def run_rings(args):
         step()
     torch.cuda.synchronize()
     tcq_proto.LAUNCH_EVENTS, tcq_proto.LAUNCH_SAMPLE, tcq_proto._launch_count = [], 1, 0
+    tcq_proto.EVENT_FACTORY = DeviceEvent
     t0 = time.perf_counter()
     for _ in range(args.steps):
         out = step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     evs, tcq_proto.LAUNCH_EVENTS = tcq_proto.LAUNCH_EVENTS, None
-    t_vit = sum(a.elapsed_time(b) for a, b in evs) * 1e-3 / args.steps
+    secs, ops, n_launch = viterbi_event_totals(evs)
+    t_vit = secs / args.steps
     cfg = TCQ_CONFIG[fmt_name]
     nl = 4 << len(cfg.get("m_extra", ()))
-    n_rings = W.numel() // 256
-    ops = n_rings * RING_SCALES * 2 * 256 * LANE_OPS_PER_STEP[int(cfg.get("pp", 0))] * 1024 * (cfg.get("n_cand", 0) or (1 << cfg["h"]))
-    achieved = ops / t_vit / 1e12
+    achieved = ops / secs / 1e12
     value = W.numel() / (dt / args.steps) / 1e6
     pub = RING_PUBLISHED.get(fmt_name)
     res = {
@@ -371,12 +444,13 @@ def run_rings(args):
         "config": {"workload": f"C5 row table {rows}x{C5_COLS} {fmt_name} rings: FWHT-256 per ring, 3 fp16 scales "
                                f"x two-pass tail-biting Viterbi (tb_window 0), selection, ring records",
                    "format": fmt_name, "rows": rows, "cols": C5_COLS, "parallelism": "single GPU"},
-        "roofline": {"bound": "valu", "timed_on": "HIP events around every Viterbi launch of the timed steps",
+        "roofline": {"bound": "valu", "timed_on": "HIP start / stop events carried by the first and last launch "
+                                                  "of every Viterbi call of the timed steps (hipExtLaunchKernelGGL)",
                      "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
                      "unit": "TFLOP/s (fp32 VALU lane-ops/s x 1e-12)", "frac": round(achieved / VALU_PEAK_TOPS, 4),
                      "traffic": None, "kernel": f"tcq_viterbi_kernel<10,2,{int(cfg.get('pp', 0))},{nl},{8 if int(cfg.get('pp', 0)) == 0 else 1}>",
                      "viterbi_ms_per_step": round(t_vit * 1e3, 2),
-                     "viterbi_launches_per_step": len(evs) // args.steps},
+                     "viterbi_launches_per_step": n_launch // args.steps},
         "breakdown": {"mvalues_s_viterbi": round(W.numel() / t_vit / 1e6, 3), "bits_per_value": out[1]},
     }
     if args.cpu_seconds > 0:
@@ -447,24 +521,14 @@ def run_experts(args):
         step()
     torch.cuda.synchronize()
     tcq_proto.LAUNCH_EVENTS, tcq_proto.LAUNCH_SAMPLE, tcq_proto._launch_count = [], 1, 0
+    tcq_proto.EVENT_FACTORY = DeviceEvent
     t0 = time.perf_counter()
     for _ in range(args.steps):
         out_gu, out_dn, packed = step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     evs, tcq_proto.LAUNCH_EVENTS = tcq_proto.LAUNCH_EVENTS, None
-    durs = [a.elapsed_time(b) * 1e-3 for a, b in evs]
-    cfg = TCQ_CONFIG[C4_FORMAT]
-    G = cfg["n_cand"]
-    # launches alternate pass 1 (64 steps) and pass 2 (256 steps); gate_up launches cover n_exp x 96 tiles,
-    # down launches n_exp x 128 tiles
-    n_gu = 2 * (C4_HIDDEN // 256) * 16
-    ops = 0.0
-    for i in range(len(durs)):
-        k = i % (n_gu + 2 * (C4_INTER // 256) * 16)
-        tiles = n_exp * (2 * C4_INTER // 16 if k < n_gu else C4_HIDDEN // 16)
-        ops += tiles * (2 * TB_WINDOW if i % 2 == 0 else 256) * LANE_OPS_PER_STEP[2] * 1024 * G
-    t_vit = sum(durs)
+    t_vit, ops, n_launch = viterbi_event_totals(evs)
     achieved = ops / t_vit / 1e12
     weights = n_exp * (2 * C4_INTER * C4_HIDDEN + C4_HIDDEN * C4_INTER)
     value = weights / (dt / args.steps) / 1e6
@@ -482,12 +546,13 @@ def run_experts(args):
                                f"damping 0.2, LDLQ on; one step = quantize_experts for both shapes (one Viterbi "
                                f"launch per sub-block over all experts' tiles) with PACK + .ltq slices",
                    "format": C4_FORMAT, "experts": n_exp, "parallelism": "single GPU"},
-        "roofline": {"bound": "valu", "timed_on": "HIP events around every Viterbi launch of the timed steps",
+        "roofline": {"bound": "valu", "timed_on": "HIP start / stop events carried by the first and last launch "
+                                                  "of every Viterbi call of the timed steps (hipExtLaunchKernelGGL)",
                      "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
                      "unit": "TFLOP/s (fp32 VALU lane-ops/s x 1e-12)", "frac": round(achieved / VALU_PEAK_TOPS, 4),
                      "traffic": None, "kernel": "tcq_viterbi_kernel<10,2,2,16,1>",
                      "viterbi_ms_per_step": round(t_vit / args.steps * 1e3, 2),
-                     "viterbi_launches_per_step": len(durs) // args.steps},
+                     "viterbi_launches_per_step": n_launch // args.steps},
         "breakdown": {"mweights_s_viterbi": round(weights / (t_vit / args.steps) / 1e6, 3),
                       "h_build_ms": round(t_h, 2), "proxy_rel_loss_mean": round(sum(rel) / len(rel), 6),
                       "packed_bytes": int(sum(p.numel() for p in packed))},
@@ -561,6 +626,7 @@ def main():
     # do not perturb the launch stream; events around the rotation, row-scale, pack and LDLQ-update calls
     timer.active = True
     liqk.STAGE_EVENTS, tcq_proto.LAUNCH_EVENTS = [], []
+    tcq_proto.EVENT_FACTORY = DeviceEvent
     tcq_proto.LAUNCH_SAMPLE, tcq_proto._launch_count = 16, 0
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -587,15 +653,14 @@ def main():
         if name == "start":
             continue
         stages[name] = stages.get(name, 0.0) + stage_ev[i - 1][1].elapsed_time(ev) / args.steps
-    durs = [a.elapsed_time(b) * 1e-3 for a, b in launch_ev]
-    # tail-biting: launches alternate pass 1 (2 * tb_window steps) and pass 2 (256 steps) over rows / 16 tiles
-    d1, d2 = durs[0::2], durs[1::2]
-    t_p1, t_p2 = sum(d1) / len(d1), sum(d2) / len(d2)
+    # one record per sampled sub-block: both passes (2 * tb_window and 256 steps over rows / 16 tiles) between
+    # one event pair
+    secs, ops_timed, n_timed = viterbi_event_totals(launch_ev)
+    avg = secs / n_timed
     n_launch = 2 * (cols // 256) * 16
-    t_vit = (t_p1 + t_p2) / 2 * n_launch
+    t_vit = avg * n_launch
     ntile = rows // 16
-    ops = (lane_ops_per_launch(cfg, ntile, 2 * TB_WINDOW) + lane_ops_per_launch(cfg, ntile, 256)) / 2
-    avg = (t_p1 + t_p2) / 2
+    ops = ops_timed / n_timed
     achieved = ops / avg / 1e12
     traffic = read_traffic()
     t_mat = sum(stages.get(k, 0.0) for k in ("rotation", "rows", "pack")) * 1e-3
@@ -611,15 +676,15 @@ def main():
                                f"{cols // 256 * 16} two-pass Viterbi sub-blocks of {ntile} tiles, LDLQ, refit) + "
                                f".ltq slice packing",
                    "format": FORMAT, "rows": rows, "cols": cols, "parallelism": "single GPU"},
-        "roofline": {"bound": "valu", "timed_on": "HIP events around both passes of one sub-block in 16", "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
+        "roofline": {"bound": "valu", "timed_on": "HIP start / stop events carried by the two Viterbi launches of one sub-block in 16 "
+                                  "(hipExtLaunchKernelGGL)", "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
                      "unit": "TFLOP/s (fp32 VALU lane-ops/s x 1e-12)", "frac": round(achieved / VALU_PEAK_TOPS, 4),
                      "traffic": traffic, "kernel": "tcq_viterbi_kernel<10,2,2,8,1>",
-                     "avg_launch_us": round(avg * 1e6, 2), "pass1_us": round(t_p1 * 1e6, 2),
-                     "pass2_us": round(t_p2 * 1e6, 2), "lane_ops_per_launch": ops},
+                     "avg_launch_us": round(avg * 1e6, 2), "lane_ops_per_launch": ops},
         "breakdown": {"stages_ms": {k: round(v, 3) for k, v in stages.items()},
                       "t_mat_ms": round(t_mat * 1e3, 3), "mweights_s_t_mat": round(weights / t_mat / 1e6, 3),
                       "t_vit_ms": round(t_vit * 1e3, 3), "mweights_s_viterbi": round(weights / t_vit / 1e6, 3),
-                      "viterbi_launches_per_step": n_launch, "viterbi_launches_timed": len(durs),
+                      "viterbi_launches_per_step": n_launch, "viterbi_launches_timed": n_timed,
                       "proxy_rel_loss": round(rel, 6),
                       "packed_bytes": int(packed.numel())},
         "h_build": h_build,

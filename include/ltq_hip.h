@@ -45,6 +45,14 @@ int tcq_viterbi_static(const float* x, const float* w, const float* tab, const f
 /* Size in bytes of tcq_viterbi_static's per-device scratch array. Host-only. */
 long tcq_viterbi_static_bytes(void);
 
+/* Timing hook for benchmarks; no counterpart in the reference. Arms the calling host thread's next `launches`
+ * Viterbi kernel launches (tcq_viterbi, tcq_viterbi_tb, tcq_viterbi_static): the first carries start_event, the
+ * last stop_event (hipEvent_t created by the caller, either may be null). They are launched with
+ * hipExtLaunchKernelGGL, which stamps the events with the dispatch's own start and end times, so no event
+ * packet sits between two kernels. launches = 0 disarms. Returns 0, or -1 for launches < 0. Results are not
+ * affected. */
+int ltq_viterbi_timing(void* start_event, void* stop_event, int launches);
+
 /* LUT sub-block quantization of the diagonal profile: for S sub-blocks of 16 weights xs[S, 16] with weights
  * dh[S, 16], bucket b = clamp(rint(x * inv_step + half_b), 0, nb - 1) picks a row of 64 candidates of lut[nb, 64];
  * the first candidate with the lowest sum_j dh (xs - lut[b_j][c])^2 gives out[S, 16] = lut[b_j][c]. Same

@@ -2,11 +2,17 @@
 // __global__ entry and a launcher. Each tcq_inst_*.hip instantiates the launcher for one parity mode, so the
 // variants compile in parallel.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "tcq_trellis.h"
 
 namespace ltq {
+
+// Timing hook (ltq_viterbi_timing): the start / stop events the next Viterbi launch of this thread carries, or
+// null. Launches with an event go through hipExtLaunchKernelGGL, which stamps the events with the dispatch's
+// own start and end times (no event packet between two kernels).
+void timing_take(hipEvent_t* start, hipEvent_t* stop);
 
 extern "C" __shared__ __align__(16) char ltq_dyn_smem[];
 
@@ -155,8 +161,10 @@ int launch(const TcqArgs& a, hipStream_t stream)
             static bool attr2[64] = {};
             if (const int e = set_max_lds_once(tcq_viterbi_kernel<NU, RB, MD, NL, 8>, half, attr2)) return e;
             const int threads = 64 * a.G * Geo<NU, RB>::Q;
-            hipLaunchKernelGGL((tcq_viterbi_kernel<NU, RB, MD, NL, 8>), dim3(a.N), dim3(threads), H.total, stream, a,
-                               half);
+            hipEvent_t e0 = nullptr, e1 = nullptr;
+            timing_take(&e0, &e1);
+            hipExtLaunchKernelGGL((tcq_viterbi_kernel<NU, RB, MD, NL, 8>), dim3(a.N), dim3(threads), H.total, stream,
+                                  e0, e1, 0, a, half);
             return 0;
         }
     }
@@ -165,7 +173,10 @@ int launch(const TcqArgs& a, hipStream_t stream)
     static bool attr[64] = {};
     if (const int e = set_max_lds_once(tcq_viterbi_kernel<NU, RB, MD, NL>, lds_max, attr)) return e;
     const int threads = 64 * a.G * Geo<NU, RB>::Q;
-    hipLaunchKernelGGL((tcq_viterbi_kernel<NU, RB, MD, NL>), dim3(a.N), dim3(threads), L.total, stream, a, lds_max);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    timing_take(&e0, &e1);
+    hipExtLaunchKernelGGL((tcq_viterbi_kernel<NU, RB, MD, NL>), dim3(a.N), dim3(threads), L.total, stream, e0, e1, 0,
+                          a, lds_max);
     return 0;
 }
 
@@ -181,8 +192,10 @@ int launch_tb(const TcqArgs& a1, const TcqArgs& a2, hipStream_t stream)
     static bool attr[64] = {};
     if (const int e = set_max_lds_once(tcq_viterbi_tb_kernel<NU, RB, MD, NL>, lds_max, attr)) return e;
     const int threads = 64 * a2.G * Geo<NU, RB>::Q;
-    hipLaunchKernelGGL((tcq_viterbi_tb_kernel<NU, RB, MD, NL>), dim3(a2.N), dim3(threads), total, stream, a1, a2,
-                       lds_max);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    timing_take(&e0, &e1);
+    hipExtLaunchKernelGGL((tcq_viterbi_tb_kernel<NU, RB, MD, NL>), dim3(a2.N), dim3(threads), total, stream, e0, e1,
+                          0, a1, a2, lds_max);
     return 0;
 }
 

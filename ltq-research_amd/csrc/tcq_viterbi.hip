@@ -28,6 +28,27 @@ LTQ_EXT_MD(0) LTQ_EXT_MD(1) LTQ_EXT_MD(2) LTQ_EXT_MD(3)
 #undef LTQ_EXT_MD
 #undef LTQ_EXT
 
+// timing hook: armed by ltq_viterbi_timing, consumed launch by launch on the arming thread
+namespace {
+struct Timing {
+    hipEvent_t start = nullptr, stop = nullptr;
+    int left = 0;  // launches still to go; the last one carries stop
+};
+thread_local Timing t_timing;
+}  // namespace
+
+void timing_take(hipEvent_t* start, hipEvent_t* stop)
+{
+    Timing& t = t_timing;
+    if (t.left <= 0) return;
+    *start = t.start;
+    t.start = nullptr;
+    if (--t.left == 0) {
+        *stop = t.stop;
+        t.stop = nullptr;
+    }
+}
+
 // per-device attributes of the current device, cached per device ordinal (a process may drive several GPUs)
 constexpr int kMaxDevices = 64;
 
@@ -195,4 +216,14 @@ extern "C" int tcq_viterbi_static(const float* x, const float* w, const float* t
     const int rc = tcq_dispatch(a, GpuLaunch{a, (hipStream_t)stream});
     if (rc != 0) return rc;
     return (int)hipGetLastError();
+}
+
+extern "C" int ltq_viterbi_timing(void* start_event, void* stop_event, int launches)
+{
+    if (launches < 0) return -1;
+    ltq::Timing& t = ltq::t_timing;
+    t.start = (hipEvent_t)start_event;
+    t.stop = (hipEvent_t)stop_event;
+    t.left = launches;
+    return 0;
 }

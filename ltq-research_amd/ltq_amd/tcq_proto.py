@@ -13,12 +13,44 @@ import torch
 
 from . import _lib
 
-# timing hook (off by default): a list receives (start, end) torch.cuda.Event pairs around tcq_viterbi launches,
-# recorded on the stream the kernel runs on, for launch pairs 0, LAUNCH_SAMPLE, 2 LAUNCH_SAMPLE, ... counted
-# from the last reset of _launch_count (a tail-biting call issues its two passes as one pair)
+# timing hook (off by default): a list receives one record per sampled call -- a tail-biting call (its two
+# passes back to back between one pair of events) or a single pass -- for calls 0, LAUNCH_SAMPLE,
+# 2 LAUNCH_SAMPLE, ... counted from the last reset of _launch_count. A record is a dict: "ev" (start, end)
+# torch.cuda.Event recorded on the stream the kernels run on, "tiles", "launches" ((steps, gain slots run) of
+# each pass between the events), "pp" (parity mode).
 LAUNCH_EVENTS: list | None = None
 LAUNCH_SAMPLE = 1
 _launch_count = 0
+# the hook's event type: a callable returning an object with record(stream) and elapsed_time(end) in ms
+# (torch.cuda.Event with timing when None). An object with a `handle` (its hipEvent_t) is not recorded around
+# the call but handed to the kernel launches themselves (ltq_viterbi_timing): the first launch of the call
+# stamps the start event with its dispatch start, the last one the stop event with its end.
+EVENT_FACTORY = None
+
+
+def _timed_call(fn, tiles, launches, pp):
+    """fn() between two events when the timing hook samples this call."""
+    global _launch_count
+    take = LAUNCH_EVENTS is not None and _launch_count % LAUNCH_SAMPLE == 0
+    if LAUNCH_EVENTS is not None:
+        _launch_count += 1
+    if not take:
+        return fn()
+    st = torch.cuda.current_stream()
+    mk = EVENT_FACTORY or (lambda: torch.cuda.Event(enable_timing=True))
+    e0, e1 = mk(), mk()
+    if hasattr(e0, "handle"):
+        _lib.lib().ltq_viterbi_timing(e0.handle, e1.handle, len(launches))
+        try:
+            out = fn()
+        finally:
+            _lib.lib().ltq_viterbi_timing(None, None, 0)
+    else:
+        e0.record(st)
+        out = fn()
+        e1.record(st)
+    LAUNCH_EVENTS.append({"ev": (e0, e1), "tiles": tiles, "launches": launches, "pp": pp})
+    return out
 
 
 def make_gains(h: int, step: float, device="cuda") -> torch.Tensor:
@@ -54,23 +86,12 @@ def _rows(wts: torch.Tensor | None, N: int, T: int) -> torch.Tensor | None:
     return (wts.view(1, T).expand(N, T) if wts.dim() == 1 else wts).float().contiguous()
 
 
-@torch.no_grad()
-def viterbi_ub_cuda(x: torch.Tensor, small: torch.Tensor, K: int, nu: int, m: int, gains: torch.Tensor | None = None,
-                    sub: int = 16, wts: torch.Tensor | None = None, init_state: torch.Tensor | None = None,
-                    return_end_state: bool = False, small_hi: torch.Tensor | None = None,
-                    gains_hi: torch.Tensor | None = None, mix: int = 0, n_cand: int = 0, return_code: bool = False,
-                    tail_biting: bool = False, tb_passes: int = 2, tb_cand1: int = 0, tb_window: int = 0,
-                    m_extra: tuple = (), pair_parity=False, _mid: int = 0, _tail: bool = False, _steps: int = 0,
-                    _rot: int = 0, _raw_code: bool = False, _fuse: bool = False, _fused: tuple | None = None):
-    """Joint (gain, trellis) Viterbi over tiles x [N, T] on the GPU; see src/tcq_proto.py:567-583 for the meaning
-    of every argument. Returns rec [N, T]; or (rec, gain index, level index) with return_code; or (rec, end
-    state) with return_end_state; or (rec, mid state) for an internal first tail-biting pass. _raw_code with
-    return_code gives (rec, code) with the kernel's packed int32 code (gain index << 16 | level index).
-    _fuse=True runs both tail-biting passes (same gain slots) in one launch (tcq_viterbi_tb, identical results).
-    It is off by default: on gfx950 the fused kernel measures ~30 us slower per 4096-tile sub-block than the two
-    launches (the pass loop keeps both argument sets live, 140 SGPR spills)."""
-    _lib.require_device(x)
-    if tail_biting:
+def _tail_biting(x, small, K, nu, m, gains, sub, wts, small_hi, gains_hi, mix, n_cand, return_code, tb_passes,
+                 tb_cand1, tb_window, m_extra, pair_parity, _raw_code, _fuse):
+    """The two-pass tail-biting driver (src/tcq_proto.py:584-609); the single passes run with the hook off."""
+    global LAUNCH_EVENTS
+    saved, LAUNCH_EVENTS = LAUNCH_EVENTS, None
+    try:
         N, T = x.shape
         h = T // 2
         common = dict(sub=sub, small_hi=small_hi, gains_hi=gains_hi, mix=mix, m_extra=m_extra, pair_parity=pair_parity)
@@ -100,7 +121,35 @@ def viterbi_ub_cuda(x: torch.Tensor, small: torch.Tensor, K: int, nu: int, m: in
                                       return_code=return_code, _tail=True, _rot=shift, _raw_code=_raw_code,
                                       **common)
         return out
+    finally:
+        LAUNCH_EVENTS = saved
 
+
+@torch.no_grad()
+def viterbi_ub_cuda(x: torch.Tensor, small: torch.Tensor, K: int, nu: int, m: int, gains: torch.Tensor | None = None,
+                    sub: int = 16, wts: torch.Tensor | None = None, init_state: torch.Tensor | None = None,
+                    return_end_state: bool = False, small_hi: torch.Tensor | None = None,
+                    gains_hi: torch.Tensor | None = None, mix: int = 0, n_cand: int = 0, return_code: bool = False,
+                    tail_biting: bool = False, tb_passes: int = 2, tb_cand1: int = 0, tb_window: int = 0,
+                    m_extra: tuple = (), pair_parity=False, _mid: int = 0, _tail: bool = False, _steps: int = 0,
+                    _rot: int = 0, _raw_code: bool = False, _fuse: bool = False, _fused: tuple | None = None):
+    """Joint (gain, trellis) Viterbi over tiles x [N, T] on the GPU; see src/tcq_proto.py:567-583 for the meaning
+    of every argument. Returns rec [N, T]; or (rec, gain index, level index) with return_code; or (rec, end
+    state) with return_end_state; or (rec, mid state) for an internal first tail-biting pass. _raw_code with
+    return_code gives (rec, code) with the kernel's packed int32 code (gain index << 16 | level index).
+    _fuse=True runs both tail-biting passes (same gain slots) in one launch (tcq_viterbi_tb, identical results).
+    It is off by default: on gfx950 the fused kernel measures ~30 us slower per 4096-tile sub-block than the two
+    launches (the pass loop keeps both argument sets live, 140 SGPR spills)."""
+    _lib.require_device(x)
+    if tail_biting:
+        N, T = x.shape
+        G_run = n_cand if 0 < n_cand < (gains.numel() if gains is not None else 1) else (
+            gains.numel() if gains is not None else 1)
+        G1 = tb_cand1 if tb_cand1 else G_run
+        launches = [(2 * tb_window if tb_window else T, G1)] + [(T, G_run)] * (tb_passes - 1)
+        return _timed_call(lambda: _tail_biting(x, small, K, nu, m, gains, sub, wts, small_hi, gains_hi, mix, n_cand,
+                                                return_code, tb_passes, tb_cand1, tb_window, m_extra, pair_parity,
+                                                _raw_code, _fuse), N, launches, int(pair_parity))
     N, ld = x.shape
     T = _steps or ld
     S, U = 1 << nu, 1 << (K - 1)
@@ -133,32 +182,25 @@ def viterbi_ub_cuda(x: torch.Tensor, small: torch.Tensor, K: int, nu: int, m: in
     cand = torch.empty((N, T // sub, G_run), dtype=torch.uint8, device=dev) if G_run < Gfull else None
     me = (list(m_extra) + [0, 0, 0])[:3]
     p = _lib.ptr
-    evs = None
-    if LAUNCH_EVENTS is not None:
-        global _launch_count
-        if (_launch_count // 2) % LAUNCH_SAMPLE == 0:
-            evs = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            evs[0].record(torch.cuda.current_stream())
-        _launch_count += 2 if _fused else 1
     mix_arg = mix if small_hi is not None else 0
-    if _fused:  # both tail-biting passes: pass 1's middle states land in mid_buf, the closing pass starts there
-        if init_state is not None:
-            raise ValueError("the fused tail-biting launch computes its own start states")
-        mid_buf = torch.empty(N, dtype=torch.int32, device=dev)
-        rc = _lib.lib().tcq_viterbi_tb(p(xf), p(w), p(tab), p(g), p(rec), p(bp), p(gsel), p(mid_buf), p(end),
-                                       p(tab_hi), p(g_hi), p(cand), p(best), p(code), int(_tail), N, T, S, U, G_run,
-                                       Gfull, m, sub, tab_hi.numel() // nl, mix_arg, me[0], me[1], me[2], nl, ld, _rot,
-                                       p(pbits), pp, _fused[0], _fused[1], _fused[2], _lib.stream_ptr())
-    else:
-        rc = _lib.lib().tcq_viterbi(p(xf), p(w), p(tab), p(g), p(rec), p(bp), p(gsel), p(init), p(end), p(tab_hi),
-                                    p(g_hi), p(cand), p(best), p(code), p(mid), _mid, int(_tail), N, T, S, U, G_run,
-                                    Gfull, m, sub, tab_hi.numel() // nl, mix_arg, me[0], me[1], me[2], nl, ld, _rot,
-                                    p(pbits), pp, _lib.stream_ptr())
+    def launch():
+        if _fused:  # both tail-biting passes: pass 1's middle states land in mid_buf, the closing pass starts there
+            if init_state is not None:
+                raise ValueError("the fused tail-biting launch computes its own start states")
+            mid_buf = torch.empty(N, dtype=torch.int32, device=dev)
+            return _lib.lib().tcq_viterbi_tb(p(xf), p(w), p(tab), p(g), p(rec), p(bp), p(gsel), p(mid_buf), p(end),
+                                             p(tab_hi), p(g_hi), p(cand), p(best), p(code), int(_tail), N, T, S, U,
+                                             G_run, Gfull, m, sub, tab_hi.numel() // nl, mix_arg, me[0], me[1], me[2],
+                                             nl, ld, _rot, p(pbits), pp, _fused[0], _fused[1], _fused[2],
+                                             _lib.stream_ptr())
+        return _lib.lib().tcq_viterbi(p(xf), p(w), p(tab), p(g), p(rec), p(bp), p(gsel), p(init), p(end), p(tab_hi),
+                                      p(g_hi), p(cand), p(best), p(code), p(mid), _mid, int(_tail), N, T, S, U, G_run,
+                                      Gfull, m, sub, tab_hi.numel() // nl, mix_arg, me[0], me[1], me[2], nl, ld, _rot,
+                                      p(pbits), pp, _lib.stream_ptr())
+
+    rc = _timed_call(launch, N, [(_fused[0], G_run), (T, G_run)] if _fused else [(T, G_run)], pp)
     if rc != 0:
         raise RuntimeError(f"tcq_viterbi: HIP error code {rc}")
-    if evs is not None:
-        evs[1].record(torch.cuda.current_stream())
-        LAUNCH_EVENTS.append(evs)
     if _mid:
         return rec, mid
     if return_code:

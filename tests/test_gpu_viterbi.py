@@ -216,3 +216,34 @@ def test_gpu_fused_tail_biting_equals_two_launches(name, window):
     torch.cuda.synchronize()
     assert torch.equal(a[0].view(torch.int32), b[0].view(torch.int32))
     assert torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])
+
+
+def test_gpu_timing_hook_keeps_results_and_times_the_launches(tp):
+    """The benchmark's timing hook (events handed to the launches through ltq_viterbi_timing) leaves the results
+    bit-identical, stamps both events, and a later call without the hook is not stamped."""
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+    import bench
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn((64, 256), generator=g) * 1.3).to(DEV)
+    w = (torch.rand((256,), generator=g) + 0.5).to(DEV)
+    lut = torch.randn(32, generator=g).to(DEV)
+    gains = tp.make_gains(2, 0.22, DEV)
+    kw = dict(sub=16, wts=w, tail_biting=True, tb_window=32, m_extra=(241,), pair_parity=2, return_code=True)
+    ref = tp.viterbi_ub_cuda(x, lut, 3, 10, 359, gains, **kw)
+    tp.LAUNCH_EVENTS, tp.LAUNCH_SAMPLE, tp._launch_count, tp.EVENT_FACTORY = [], 1, 0, bench.DeviceEvent
+    try:
+        out = tp.viterbi_ub_cuda(x, lut, 3, 10, 359, gains, **kw)
+        recs = tp.LAUNCH_EVENTS
+    finally:
+        tp.LAUNCH_EVENTS, tp.EVENT_FACTORY = None, None
+    again = tp.viterbi_ub_cuda(x, lut, 3, 10, 359, gains, **kw)
+    torch.cuda.synchronize()
+    for a, b, c in zip(ref, out, again):
+        assert torch.equal(a, b) and torch.equal(a, c)
+    assert len(recs) == 1 and recs[0]["launches"] == [(64, 4), (256, 4)]
+    e0, e1 = recs[0]["ev"]
+    ms = e0.elapsed_time(e1)
+    print(f"two passes over 64 tiles: {ms * 1e3:.1f} us", flush=True)
+    assert 0.0 < ms < 50.0
