@@ -50,6 +50,8 @@ struct GpuX {
     }
     // v is computed at this point (not sunk past it), held in a vector register
     __device__ __forceinline__ void pin(uint32_t& v) const { asm volatile("" : "+v"(v)); }
+    // v (uniform) is computed at this point, held in a scalar register
+    __device__ __forceinline__ void pin_s(uint32_t& v) const { asm volatile("" : "+s"(v)); }
     // (value, index) minimum over the wavefront, lowest index on ties, left in lane 63: DPP row operations
     // (quad swaps, half-row and row mirrors, then row broadcasts 15 and 31) instead of LDS permutes. The
     // lexicographic minimum does not depend on the order of the combines.

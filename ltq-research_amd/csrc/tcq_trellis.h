@@ -436,7 +436,8 @@ struct DecMap {
 // X provides: tid(), wave() (tid / 64, uniform), tile(), nthreads(), smem(), sync() (full barrier incl. global
 // memory), lds_sync() (barrier for LDS only), push_sign(acc, d), fmin(x, y), wave_min(v, i) (the wavefront's
 // (value, index) minimum, lowest index on ties, in lane 63), readlane(v, l) (lane l's value, l uniform), uni(v)
-// (a uniform value in a scalar register), pin(v) (v computed at this point), sched_fence() (no instruction
+// (a uniform value in a scalar register), pin(v) / pin_s(v) (v computed at this point, in a vector / scalar
+// register), sched_fence() (no instruction
 // moved across), load_coherent(p) (a global int written by this workgroup before a sync()), acquire()
 // (device-scope acquire: invalidates this CU's L1), load16(global src, LDS wave base) (asynchronous 16-byte
 // global -> LDS copy landing at base + 16 * lane), wait_loads(n) (at most n such copies of this wave still
@@ -924,7 +925,9 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
     // block; that lane's decision bits give the phase's input state, the intermediate state and the parity
     // classes. Lanes of the walking wavefront fetch the possible next lookups one phase ahead; v_readlane
     // picks the true one.
-    uint16_t* s_rec = (uint16_t*)s_st;  // per phase: output state | slot << 10 | e << 13 | classes << 14
+    // per phase: output state | slot << 10 | e << 13 | pa << 14 | (pa ^ pb) << 15 (pa, pb: the classes of steps
+    // ta, ta + 1; in D4 pa ^ pb is the class c* chosen by phase B, so a phase-B record takes its winner index as is)
+    uint16_t* s_rec = (uint16_t*)s_st;
     // Streamlined walk (whole chunks, one block per lane, a second wavefront, a ring of at least 3 chunks,
     // sub-blocks of 16 or 32; every matrix-path tile): wavefront 0 walks, wavefront 1 copies the decision words of the chunks ahead
     // global -> LDS, one barrier per chunk hands them over, and every thread writes the outputs. Otherwise
@@ -1030,19 +1033,9 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                     for (int w = 0; w < NW; w++) R[hi][w] = src[w * 64];
                 }
             };
-            auto pick_row = [&](int hi, int w) -> uint32_t {
-                if constexpr (Q == 4) {
-                    const uint32_t lo2 = (hi & 1) ? R[1][w] : R[0][w];
-                    const uint32_t hi2 = (hi & 1) ? R[3][w] : R[2][w];
-                    return (hi & 2) ? hi2 : lo2;
-                } else {
-                    uint32_t v = R[0][w];
-#pragma unroll
-                    for (int h = 1; h < Q; h++)
-                        if (hi == h) v = R[h][w];
-                    return v;
-                }
-            };
+            // row hi is uniform: the register array is indexed through the GPR index mode (s_set_gpr_idx_on /
+            // v_mov / off), four scalar + vector instructions a word instead of a three-deep v_cndmask tree
+            auto pick_row = [&](int hi, int w) -> uint32_t { return R[X_.uni(hi)][w]; };
             const bool rw = (sub % CK) == 0;
             // The walk over chunks kmax .. : MIDW (first tail-biting pass) stops at the phase holding mid_t and writes
             // no records; the full walk keeps every phase's 16-bit record in scalar registers and stores a chunk's
@@ -1056,17 +1049,22 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                 if constexpr (RW) {
                     if (wv == 0) load_regs(rslot(nchunk - 1), gs);
                 }
+                // ring slot of chunk cc, stepped down with cc (no division in the loop)
+                int si = (nchunk - 1 + roff) % nslot;
+                uint32_t* const ring0 = (uint32_t*)(sm + SM.ring);
                 for (int k = 0; k < kmax; k++) {
                     const int cc = nchunk - 1 - k;
+                    const int si_next = si == 0 ? nslot - 1 : si - 1;  // chunk cc - 1
                     if (copier) {  // chunk cc - nslot + 1 into the slot chunk cc + 1 left; chunk cc - 2 lands first
                         if (k == 0 && nres > 0) first_copies();
                         if (cc - nslot + 1 >= 0 && cc - nslot + 1 <= top_copied) issue(cc - nslot + 1);
                         X_.wait_loads(count(max_i(0, cc - nslot + 1), min_i(cc - 3, top_copied)) * my_loads);
                     }
                     if (wv == 0) {
-                        const uint32_t* slot = rslot(cc);
-                        const uint32_t* slot_next = rslot(cc + nslot - 1);  // chunk cc - 1 (same slot as cc + nslot - 1)
-                        uint32_t recs[NPC];
+                        const uint32_t* slot = ring0 + si * slot_words;
+                        const uint32_t* slot_next = ring0 + si_next * slot_words;
+                        // the chunk's records, two a word (phase 2 w + 1 in the high half), built phase by phase
+                        uint32_t recw[NPC / 2];
                         static_for<0, NPC>([&](auto Kc) {
                             constexpr int pi = NPC - 1 - decltype(Kc)::value;
                             constexpr int PT = MM::PT(pi);
@@ -1165,7 +1163,13 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                                     return;
                                 }
                             } else {
-                                recs[pi] = (uint32_t)(st | (gs << 10) | (e << 13) | (pa << 14) | (pb << 15));
+                                const uint32_t rec = (uint32_t)(st | (gs << 10) | (e << 13) | (pa << 14) | ((pa ^ pb) << 15));
+                                if constexpr (pi & 1) {
+                                    recw[pi / 2] = rec << 16;
+                                } else {
+                                    recw[pi / 2] |= rec;
+                                    X_.pin_s(recw[pi / 2]);  // built now: no per-phase fields stay live to the chunk end
+                                }
                             }
                             const int Ln = X_.uni(2 * h + e);
                             st = X_.uni(GE::start(Ln, qq, ll));  // state at step ta - 1
@@ -1176,7 +1180,9 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                                 sel = Ln + 4 * gs;
                             }
                             if constexpr (RW) {
-                                if (pi == 0 && cc > 0) load_regs(slot_next, gs);  // chunk cc - 1, the path's slot
+                                // chunk cc - 1, the path's slot (for cc = 0 an unused in-bounds copy of chunk 0's
+                                // slot: an unconditional load lands straight in R, waited for at its first use)
+                                if (pi == 0) load_regs(cc > 0 ? slot_next : slot, gs);
                             }
                         });
                         if constexpr (!MIDW) {
@@ -1184,12 +1190,13 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                                 uint32_t* dst = (uint32_t*)s_rec + cc * (NPC / 2);
                                 static_for<0, NPC / 2>([&](auto Wc) {
                                     constexpr int w = decltype(Wc)::value;
-                                    dst[w] = recs[2 * w] | (recs[2 * w + 1] << 16);
+                                    dst[w] = recw[w];
                                 });
                             }
                         }
                     }
                     X_.lds_sync();  // the records of chunk cc are written; chunk cc - 2 is in LDS; slot of cc + 1 free
+                    si = si_next;
                 }
             };
             if (a.mid_st) {
@@ -1320,7 +1327,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                 }
                 const int ph = ta >> 1;
                 // the phase's output state, slot, intermediate bit and classes (the step-ta state follows from them)
-                s_rec[ph] = (uint16_t)(st | (gs << 10) | (e << 13) | (pa << 14) | (pb << 15));
+                s_rec[ph] = (uint16_t)(st | (gs << 10) | (e << 13) | (pa << 14) | ((pa ^ pb) << 15));
                 if (ph == mid_ph) {  // first tail-biting pass: only the state before mid_t is needed
                     if (lane == 0) a.mid_st[n] = (a.mid_t - 1) & 1 ? st : GE::mid(bb, 2 * ca + e, qq, ll);
                     done = true;
@@ -1358,7 +1365,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
         const int stt = (t & 1) ? so
                                 : GE::mid(so >> (8 + QB), 2 * ((so >> 1) & 1) + ((rr >> 13) & 1), (so >> 8) & (Q - 1),
                                           (so >> 2) & 63);
-        const int par = (rr >> ((t & 1) ? 15 : 14)) & 1;
+        const int par = ((rr >> 14) ^ ((t & 1) ? rr >> 15 : 0)) & 1;  // pa, or pb = pa ^ (pa ^ pb)
         const int lb = mk.label(stt);
         const bool hi = mix > 0 && ((t / mix) & 1);
         const int Ut = hi ? U_hi : U;

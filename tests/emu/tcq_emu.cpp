@@ -65,6 +65,7 @@ struct CpuX {
     void sched_fence() const {}
     int opaque_zero() const { return 0; }
     void pin(uint32_t&) const {}
+    void pin_s(uint32_t&) const {}
     // (value, index) minimum over the wavefront, lowest index on ties, in every lane (the GPU leaves it in lane 63)
     void wave_min(float& bv, int& bi) const
     {
