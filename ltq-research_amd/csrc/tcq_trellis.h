@@ -499,17 +499,35 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
 
     // ---- gain candidates: the G gains of lowest scalar error per sub-block (tcq_viterbi.cu:155-180) ----
     if (cand) {
-        for (int i = tid; i < nsub * Gf; i += nthr) {
-            const int j = i / Gf, gi = i % Gf;
-            float e = 0.f;
-            for (int t = j * sub; t < (j + 1) * sub; t++) {
-                const bool hi = mix > 0 && ((t / mix) & 1);
-                const float be = hi ? level_err(s_x[t], s_gain_hi[gi], s_tab_hi, 0, NL * U_hi, 1)
-                                    : level_err(s_x[t], s_gain[gi], s_tab, 0, NL * U, 1);
-                const float prod = be * s_w[t];
-                e = e + prod;
+        // The (step, gain) products fl(level_err * w) are independent: every thread computes some of them into
+        // the forward pass's LDS (free until tables(0)), then each (sub-block, gain) sums its steps in order, as
+        // the reference's loop does (identical fp32 operations). A tile too large for that LDS (never a
+        // production shape) runs the loop as written.
+        const int nprod = nsub * sub * Gf;
+        const int room = (SM.exch - SM.tabs) / 4 + (SM.dbl ? 2 : 1) * SM.exch_floats;
+        auto prod_of = [&](int t, int gi) {
+            const bool hi = mix > 0 && ((t / mix) & 1);
+            const float be = hi ? level_err(s_x[t], s_gain_hi[gi], s_tab_hi, 0, NL * U_hi, 1)
+                                : level_err(s_x[t], s_gain[gi], s_tab, 0, NL * U, 1);
+            return be * s_w[t];
+        };
+        if (nprod <= room) {
+            float* s_prod = s_tabs;  // [t][gi]
+            for (int i = tid; i < nprod; i += nthr) s_prod[i] = prod_of(i / Gf, i % Gf);
+            X_.lds_sync();
+            for (int i = tid; i < nsub * Gf; i += nthr) {
+                const int j = i / Gf, gi = i % Gf;
+                float e = 0.f;
+                for (int t = j * sub; t < (j + 1) * sub; t++) e = e + s_prod[t * Gf + gi];
+                s_ce[i] = e;
             }
-            s_ce[i] = e;
+        } else {
+            for (int i = tid; i < nsub * Gf; i += nthr) {
+                const int j = i / Gf, gi = i % Gf;
+                float e = 0.f;
+                for (int t = j * sub; t < (j + 1) * sub; t++) e = e + prod_of(t, gi);
+                s_ce[i] = e;
+            }
         }
         X_.lds_sync();
         if (tid < nsub) {
