@@ -12,6 +12,12 @@
                    Replaces solve_triangular(L, I) (src/liqk_v2.py:1081).
   spd_solve        A x = b through cholesky_lower and two blocked substitutions; falls back to the LU solve
                    of src/liqk_v2.py:1163 when A is not numerically positive definite.
+  cholesky_many    the factors of a batch of matrices of up to `leaf` rows in one batched device call (MoE
+                   experts: 128 factorizations of 2048 rows take 16 ms against 6 ms each one by one). The
+                   device's batched potrf (MAGMA) gives each matrix the same bits whatever batch it is in (two or
+                   more), but its single-matrix potrf is another algorithm; so a lone matrix up to `leaf` rows
+                   is factored as a batch of two (itself twice), and a matrix factors to the same bits alone or
+                   in a batch.
 
 All results agree with the unblocked routines to fp32 rounding (the order of the sums differs, as it does
 between any two BLAS libraries).
@@ -48,7 +54,20 @@ def _magma_cholesky(A: torch.Tensor):
         torch.backends.cuda.preferred_linalg_library(prev)
 
 
-def cholesky_lower(A: torch.Tensor, leaf: int = 2048, magma: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
+LEAF = 2048
+
+
+def cholesky_many(A: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(L, info) [B, n, n], [B] for symmetric A [B, n, n] (lower triangles read), n <= LEAF: one batched call; on
+    the device a batch of one goes as a batch of two, so each factor has the bits of the batched algorithm."""
+    if A.is_cuda and A.shape[0] == 1:
+        L, info = torch.linalg.cholesky_ex(A.expand(2, -1, -1).contiguous())
+        return L[:1], info[:1].to(torch.int64)
+    L, info = torch.linalg.cholesky_ex(A)
+    return L, info.to(torch.int64)
+
+
+def cholesky_lower(A: torch.Tensor, leaf: int = LEAF, magma: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
     """(L, info): lower Cholesky factor of symmetric A (only its lower triangle is read) and an int tensor that is
     0 when the factorization succeeded."""
     n = A.shape[0]
@@ -57,8 +76,8 @@ def cholesky_lower(A: torch.Tensor, leaf: int = 2048, magma: bool = True) -> Tup
         if r is not None:
             return r
     if n <= leaf:
-        L, info = torch.linalg.cholesky_ex(A)
-        return L, info.to(torch.int64)
+        L, info = cholesky_many(A.unsqueeze(0))
+        return L[0], info[0]
     h = _split(n)
     L = torch.zeros_like(A)
     L11, i1 = cholesky_lower(A[:h, :h], leaf, False)
@@ -181,7 +200,12 @@ def gram_lower(A: torch.Tensor, B: torch.Tensor, nb: int = 2048) -> torch.Tensor
 def spd_solve(A: torch.Tensor, b: torch.Tensor, nb: int = 512) -> torch.Tensor:
     """x with A x = b for symmetric positive definite A [n, n] (only its lower triangle is read), b [n]; LU solve
     of the symmetric matrix when the Cholesky fails."""
-    L, info = cholesky_lower(A)
+    return spd_solve_factored(A, b, *cholesky_lower(A), nb=nb)
+
+
+def spd_solve_factored(A: torch.Tensor, b: torch.Tensor, L: torch.Tensor, info: torch.Tensor,
+                       nb: int = 512) -> torch.Tensor:
+    """spd_solve with A's Cholesky factor (L, info) already computed (e.g. by cholesky_many)."""
     if int(info.item()) != 0:
         full = torch.tril(A) + torch.tril(A, -1).T
         return torch.linalg.solve(full, b)

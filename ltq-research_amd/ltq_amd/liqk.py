@@ -19,7 +19,7 @@ from __future__ import annotations
 
 import os
 from dataclasses import dataclass
-from typing import Dict, List, Optional, Tuple
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
 
@@ -49,19 +49,19 @@ def _check(rc: int, what: str) -> None:
 
 
 @torch.no_grad()
-def factor_hessian(H_rot: torch.Tensor, damp: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(U, diag_w, U_blks_inv): U upper Cholesky factor of H^-1 (U^T U = H^-1) from one factorization of the
-    flipped, damped H and one triangular inversion; diag_w = 1 / diag(U)^2; inverses of U's 256 x 256 diagonal
-    blocks."""
-    K = H_rot.shape[0]
-    nblocks = K // QK_K
+def _damped_flip(H_rot: torch.Tensor, damp: float) -> torch.Tensor:
+    """The matrix factor_hessian factors: H + damp mean(diag H) I, rows and columns reversed."""
     H_reg = H_rot.float().clone()
     diag_mean = H_reg.diagonal().mean().clamp(min=1e-8)
     H_reg.diagonal().add_(damp * diag_mean)
-    L_flip, info = linalg.cholesky_lower(H_reg.flip(0, 1).contiguous())
-    del H_reg
+    return H_reg.flip(0, 1).contiguous()
+
+
+def _factors_from(L_flip: torch.Tensor, info: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(U, diag_w, U_blks_inv) from the Cholesky factor of the flipped, damped H."""
     if int(info.item()) != 0:
         raise torch.linalg.LinAlgError("factor_hessian: the damped Hessian is not positive definite")
+    nblocks = L_flip.shape[0] // QK_K
     U = linalg.tri_inv_lower(L_flip).flip(0, 1).contiguous()  # the kernels take row-major factors
     diag_w = 1.0 / (torch.diagonal(U) ** 2).clamp(min=1e-12)
     # U = J L'^-1 J (J reverses the order), so U's diagonal block b is J (L'_cc)^-1 J with c = nblocks - 1 - b
@@ -69,8 +69,33 @@ def factor_hessian(H_rot: torch.Tensor, damp: float) -> Tuple[torch.Tensor, torc
     # them numerically)
     U_blks_inv = torch.stack([L_flip[c * QK_K:(c + 1) * QK_K, c * QK_K:(c + 1) * QK_K]
                               for c in range(nblocks - 1, -1, -1)]).flip(1, 2).contiguous()
-    del L_flip
     return U, diag_w, U_blks_inv
+
+
+def factor_hessian(H_rot: torch.Tensor, damp: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(U, diag_w, U_blks_inv): U upper Cholesky factor of H^-1 (U^T U = H^-1) from one factorization of the
+    flipped, damped H and one triangular inversion; diag_w = 1 / diag(U)^2; inverses of U's 256 x 256 diagonal
+    blocks."""
+    return _factors_from(*linalg.cholesky_lower(_damped_flip(H_rot, damp)))
+
+
+def factor_hessians(H_rots: Sequence[torch.Tensor], damp: float) -> List[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]]:
+    """factor_hessian of each matrix, bit for bit; the factorizations of same-sized matrices of up to
+    linalg.LEAF rows go through one batched call (linalg.cholesky_many)."""
+    out: List = [None] * len(H_rots)
+    by_size: Dict[int, List[int]] = {}
+    for i, H in enumerate(H_rots):
+        by_size.setdefault(H.shape[0], []).append(i)
+    for K, idx in by_size.items():
+        if K > linalg.LEAF or not H_rots[idx[0]].is_cuda:
+            for i in idx:
+                out[i] = factor_hessian(H_rots[i], damp)
+            continue
+        L, info = linalg.cholesky_many(torch.stack([_damped_flip(H_rots[i], damp) for i in idx]))
+        for j, i in enumerate(idx):
+            out[i] = _factors_from(L[j], info[j])
+        del L
+    return out
 
 
 _EXP2_TABS: Dict[tuple, torch.Tensor] = {}
@@ -260,6 +285,12 @@ def refit_scales(W: torch.Tensor, H: torch.Tensor, HW: torch.Tensor, U_base: tor
     reconstruction is U_base * suh), the per-(row, block) scales d [M, nblk] fp16 and the normalized row weights
     rw [M] (None: unweighted). Returns (the record, the reconstruction W_hat of the scales the record chose,
     W_hat H): (c_eff U_base) * suh_cand when accepted, else U_base * suh."""
+    st = _refit_prepare(W, H, HW, U_base, suh, d, rw)
+    return _refit_finish(st, linalg.cholesky_lower(st["A"]), keep)
+
+
+def _refit_prepare(W, H, HW, U_base, suh, d, rw) -> dict:
+    """The refit up to its SPD system: c_row, the new block scales, A (lower triangle, ridge included), b."""
     W_hat = U_base * suh.unsqueeze(0)
     HQ = W_hat @ H
     gain_num = (W_hat * HW).sum(dim=1)
@@ -279,22 +310,50 @@ def refit_scales(W: torch.Tensor, H: torch.Tensor, HW: torch.Tensor, U_base: tor
     A.diagonal().add_(1e-3 * A.diagonal().mean().clamp(min=1e-12))
     weight = torch.ones_like(c_row) if rw is None else rw
     loss_base = float((row_proxy(HW, HQ, W, W_hat) * weight).sum().item())
+    return dict(W=W, H=H, HW=HW, suh=suh, W_hat=W_hat, HQ=HQ, c_raw=c_raw, c_row=c_row, d_new=d_new, c_eff=c_eff,
+                U_s=U_s, A=A, b=b, weight=weight, loss_base=loss_base)
+
+
+def _refit_finish(st: dict, factor, keep: bool = False) -> Tuple[RefitResult, torch.Tensor, torch.Tensor]:
+    """The refit from A's Cholesky factor (L, info): solve, fp16 candidate scales, loss, acceptance."""
+    W, H, HW, suh, A, b = st["W"], st["H"], st["HW"], st["suh"], st["A"], st["b"]
     s_solved, suh_cand, loss_cand, W_cand, HQ_cand = None, suh, float("inf"), None, None
     try:
-        s_solved = linalg.spd_solve(A, b)
+        s_solved = linalg.spd_solve_factored(A, b, *factor)
     except RuntimeError:  # a singular system leaves the scales as they are (src/liqk_v2.py:1179-1180)
         pass
     if s_solved is not None:
         s16 = s_solved.to(torch.float16).to(torch.float32)
         good = torch.isfinite(s16) & (s16.abs() > 0.05) & (s16.abs() < 10.0)
         suh_cand = torch.where(good, s16, suh)
-        W_cand = U_s * suh_cand.unsqueeze(0)
+        W_cand = st["U_s"] * suh_cand.unsqueeze(0)
         HQ_cand = W_cand @ H
-        loss_cand = float((row_proxy(HW, HQ_cand, W, W_cand) * weight).sum().item())
-    accepted = loss_cand < loss_base
-    rec = RefitResult(c_raw, c_row, d_new, c_eff, A if keep else None, b, s_solved, suh_cand, loss_base, loss_cand,
-                      accepted)
-    return (rec, W_cand, HQ_cand) if accepted else (rec, W_hat, HQ)
+        loss_cand = float((row_proxy(HW, HQ_cand, W, W_cand) * st["weight"]).sum().item())
+    accepted = loss_cand < st["loss_base"]
+    rec = RefitResult(st["c_raw"], st["c_row"], st["d_new"], st["c_eff"], A if keep else None, b, s_solved, suh_cand,
+                      st["loss_base"], loss_cand, accepted)
+    return (rec, W_cand, HQ_cand) if accepted else (rec, st["W_hat"], st["HQ"])
+
+
+def refit_jobs(jobs: Sequence["_MatrixJob"]) -> None:
+    """job.refit() for each job, bit for bit, with the SPD systems of same-sized matrices of up to linalg.LEAF
+    rows factored in one batched call."""
+    As = [j.refit_prepare() for j in jobs]
+    by_size: Dict[int, List[int]] = {}
+    for i, A in enumerate(As):
+        by_size.setdefault(A.shape[0], []).append(i)
+    factors: List = [None] * len(jobs)
+    for K, idx in by_size.items():
+        if K > linalg.LEAF or not As[idx[0]].is_cuda:
+            for i in idx:
+                factors[i] = linalg.cholesky_lower(As[i])
+            continue
+        L, info = linalg.cholesky_many(torch.stack([As[i] for i in idx]))
+        for j, i in enumerate(idx):
+            factors[i] = (L[j], info[j])
+    del As
+    for j, f in zip(jobs, factors):
+        j.refit_finish(f)
 
 
 def _row_slices(spec_or_row_specs, M: int) -> List[Tuple[int, int, str]]:
@@ -329,12 +388,17 @@ class _MatrixJob:
         self.row_weights = row_weights
 
     def rotate_and_factor(self):
-        self.W_rot, H_rot, self.suh = rotation.compute_optimal_suh(self.W, self.H, seed=self.seed,
-                                                                   row_weights=self.row_weights)
-        _mark("rotation")
+        H_rot = self.rotate()
         self.U, self.diag_w, self.U_blks_inv = factor_hessian(H_rot, self.damp)
         del H_rot
         _mark("factor")
+
+    def rotate(self) -> torch.Tensor:
+        """The rotation and suh; returns the rotated Hessian for the factorization."""
+        self.W_rot, H_rot, self.suh = rotation.compute_optimal_suh(self.W, self.H, seed=self.seed,
+                                                                   row_weights=self.row_weights)
+        _mark("rotation")
+        return H_rot
 
     def quantize_groups(self):
         """Each format's rows through the LDLQ loop; with PACK, the tile fields gathered into matrix order."""
@@ -360,12 +424,21 @@ class _MatrixJob:
         _mark("rows")
 
     def refit(self):
+        self.refit_finish(linalg.cholesky_lower(self.refit_prepare()))
+
+    def refit_prepare(self) -> torch.Tensor:
+        """The refit up to its SPD system; returns the system's matrix (lower triangle) to factor."""
         self.HW = self.W @ self.H
         U_base = rotation.fwht_inplace(self.W_hat_rot, block_size=QK_K)
         rw = None
         if self.row_weights is not None:
             rw = rotation.normalized_row_weights(self.row_weights.to(self.W.device)).float()
-        rec, self.W_hat, self.HQ = refit_scales(self.W, self.H, self.HW, U_base, self.suh, self.d, rw)
+        self._refit = _refit_prepare(self.W, self.H, self.HW, U_base, self.suh, self.d, rw)
+        return self._refit["A"]
+
+    def refit_finish(self, factor):
+        rec, self.W_hat, self.HQ = _refit_finish(self._refit, factor)
+        del self._refit
         global LAST_REFIT
         LAST_REFIT = rec
         self.c_pack = torch.ones(self.M, device=self.W.device)

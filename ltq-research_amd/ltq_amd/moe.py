@@ -4,10 +4,12 @@ the Viterbi work of all experts in shared launches.
 The reference quantizes the experts one by one (src/streaming_quant.py:262-276: gate_up_proj [2 I, H] with the
 expert's input Hessian, down_proj [H, I] with the Hessian of its intermediate activations, each a full
 quantize_matrix_liqk_v2 call with seed _seed(layer, name), src/streaming_quant.py:116-117, 130-133). Here the
-per-expert stages that are matrix-sized linear algebra (rotation, Hessian factorization, refit, PACK fields)
-run per expert through the same code as a single matrix, while the row quantizer's LDLQ loop runs once for
-all same-shaped experts stacked along rows: one two-pass Viterbi launch per 16-column sub-block covers the tiles
-of every expert, and the LDLQ kernels read each tile's own expert factors (ltq_ldlq_* with matrix strides). Rows
+per-expert stages that are matrix-sized linear algebra (rotation, refit, PACK fields) run per expert through
+the same code as a single matrix, with the Cholesky factorizations of all experts (the Hessians' and the refits'
+SPD systems) each in one batched call, which factors every matrix to the bits it gets alone
+(liqk.factor_hessians, liqk.refit_jobs, linalg.cholesky_many). The row quantizer's LDLQ loop runs once for all
+same-shaped experts stacked along rows: one two-pass Viterbi launch per 16-column sub-block covers the tiles of
+every expert, and the LDLQ kernels read each tile's own expert factors (ltq_ldlq_* with matrix strides). Rows
 are independent in that loop, so every expert's codes, scales and reconstruction equal those of its own call.
 """
 from __future__ import annotations
@@ -43,11 +45,16 @@ def quantize_experts(Ws: Sequence[torch.Tensor], Hs: Sequence[torch.Tensor], spe
         raise ValueError("quantize_experts: rows per expert must be a multiple of 128 to share launches")
     packing = liqk.PACK is not None
     liqk._mark("start")
-    jobs = []
+    jobs, H_rots = [], []
     for W, H, seed in zip(Ws, Hs, seeds):
         job = liqk._MatrixJob(W, H, [(0, R, spec)], seed, damp, None)
-        job.rotate_and_factor()
+        H_rots.append(job.rotate())
         jobs.append(job)
+    # the experts' factorizations in one batched call (bit-identical to factoring each alone)
+    for job, (U, dw, Ubi) in zip(jobs, liqk.factor_hessians(H_rots, jobs[0].damp)):
+        job.U, job.diag_w, job.U_blks_inv = U, dw, Ubi
+    del H_rots
+    liqk._mark("factor")
     # the rows stage of all experts at once
     W_rot = torch.cat([j.W_rot for j in jobs], dim=0)
     U = torch.stack([j.U for j in jobs])
@@ -70,7 +77,8 @@ def quantize_experts(Ws: Sequence[torch.Tensor], Hs: Sequence[torch.Tensor], spe
         if packing:
             job.fields = {"idx": grp["idx"][rows], "gi": grp["gi"][rows], "G": grp["G"][rows],
                           "d_row": grp["d_row"][rows], "e": grp["e"][rows]}
-        job.refit()
+    liqk.refit_jobs(jobs)  # the refits' SPD systems factored in one batched call
+    for e, job in enumerate(jobs):
         if packing:
             job.write_fields()
             fields.append(liqk.PACK.pop("matrix"))
