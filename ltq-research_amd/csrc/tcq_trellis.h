@@ -560,10 +560,11 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
     const int TF = SM.tab_floats;
     auto tables = [&](int cc) {
         float* tb = s_tabs + (cc & 1) * TF;
-        // one entry per thread, the slot's own gain, two levels per parity class at most (the D4 formats with
-        // 8-subset labels, as in the matrix path): straight-line, the level loop of level_err unrolled
+        // one entry per thread (the table has 64 Q entries per gain slot: D4 and EQ with 8 labels, D2 with 4, at
+        // four wavefronts per slot), the slot's own gain (no candidates), two levels per parity class at most:
+        // straight-line, the level loop of level_err unrolled; any other launch shape takes the loop below
         if constexpr (MD != 0 && CK * NL * NP == 64 * Q) {
-            if (!cand && (U == 2 || U == 4)) {
+            if (!cand && (U == 2 || U == 4) && nthr == TF) {
                 const int e = tid;
                 const int p = e & 1, lb = (e / NP) % NL, k = (e / (NP * NL)) % CK, gg = e / (NP * NL * CK);
                 const int t = cc * CK + k;

@@ -62,6 +62,11 @@ SINGLE = [  # kwargs of one kernel call (reference ABI semantics)
     dict(nu=10, nl_ext=(), G=4, T=512, U=16, pp=0, sub=32),
     dict(nu=10, nl_ext=(), G=2, T=128, U=4, pp=0, mix=16),
     dict(nu=10, nl_ext=(40,), G=8, T=128, U=4, pp=2),
+    # the straight-line metric table with 2 levels per label and D2 / EQ shapes
+    dict(nu=10, nl_ext=(241,), G=4, T=256, U=2, pp=2),
+    dict(nu=10, nl_ext=(), G=2, T=256, U=2, pp=1),
+    dict(nu=10, nl_ext=(), G=4, T=256, U=4, pp=1),
+    dict(nu=10, nl_ext=(241,), G=2, T=256, U=2, pp=3),
 ]
 
 

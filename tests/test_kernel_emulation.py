@@ -42,6 +42,11 @@ CASES = [
     dict(pp=0, ext=(241,), G=2, T=64, sub=32),
     dict(pp=1, ext=(241,), G=4, T=64, sub=32, mid_t=40),
     dict(pp=2, ext=(241,), G=2, T=96, sub=32, init=True, tail=True),
+    # the straight-line metric table (one entry per thread: D4 / EQ with 8 labels, D2 with 4; U = 2 and 4)
+    dict(pp=2, ext=(241,), G=4, T=32, U=2),
+    dict(pp=1, ext=(), G=2, T=64, U=2),
+    dict(pp=1, ext=(), G=4, T=64, U=4),
+    dict(pp=3, ext=(241,), G=2, T=32, U=2),
 ]
 
 
