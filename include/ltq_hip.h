@@ -126,7 +126,7 @@ int ltq_pack_rings(const int16_t* idx, long ld_idx, const uint8_t* gi, long ld_g
  * rounded once to fp32 on the host (the table the .ltq decoder uses). Replaces the torch code
  * src/liqk_v2.py:938-946 (and the clamp of :959); its results are defined to the bit: fixed-order block sums
  * (per 4-element group left to right, then a lane butterfly over offsets 32..1), correctly rounded fp32 sqrt,
- * log / mean / exp and log2 in float64, round half to even. */
+ * log / mean / exp and log2 in float64, round half to even. K <= 262144. */
 int ltq_row_scale(const float* w, long M, long K, long ldw, float scale, float e_step, int e_bits,
                   const float* exp2_tab, float* d_row, int8_t* e, long lde, float* d, long ldd, void* stream);
 

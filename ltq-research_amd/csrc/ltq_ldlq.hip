@@ -7,7 +7,8 @@
 //   - block sum of squares: lane l holds ((x[4l]^2 + x[4l+1]^2) + x[4l+2]^2) + x[4l+3]^2, then a butterfly over
 //     lane offsets 32, 16, 8, 4, 2, 1 (s_l + s_(l^o): every lane ends with the same bits); rms = sqrt(s / 256),
 //     all fp32, correctly rounded;
-//   - log, mean and exp in float64 (sequential sum over the blocks), rounded to fp32 and then to fp16; the
+//   - log, mean and exp in float64 (the logs one block per lane, their sum sequential over the blocks), rounded
+//     to fp32 and then to fp16; the
 //     exponent from the fp32 ratio rms / d_row as round-half-even of log2(ratio) / e_step in float64: float64
 //     keeps every value far from the fp16 / half-step rounding boundaries the fp32 functions can straddle;
 //   - 2^(e_step e) is read from a host-computed table (float64, rounded once to fp32), the same table the PACK
@@ -40,13 +41,13 @@ __global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict_
                                                         int8_t* __restrict__ e_out, long lde, float* __restrict__ d_out,
                                                         long ldd)
 {
-    extern __shared__ float s_rms[];  // [4 waves][nblk]
+    extern __shared__ double s_dyn[];  // [4 waves][nblk] log(rms) (float64), then [4 waves][nblk] rms (fp32)
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const long row = (long)blockIdx.x * 4 + wv;
     if (row >= M) return;
-    float* rms = s_rms + wv * nblk;
+    double* lg = s_dyn + wv * nblk;
+    float* rms = (float*)(s_dyn + 4 * nblk) + wv * nblk;
     const float* wr = w + row * ldw;
-    double lsum = 0.0;
     constexpr int kAhead = 8;  // blocks whose loads are in flight together
     for (int b0 = 0; b0 < nblk; b0 += kAhead) {
         float4 v[kAhead];
@@ -65,9 +66,19 @@ __global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict_
             if (b0 + j >= nblk) break;
             const float r = fmaxf(sqrtf(s[j] / 256.f), 1e-10f) * scale;
             if (lane == 0) rms[b0 + j] = r;
-            lsum += log((double)r);  // every lane holds the same r; blocks summed in order
         }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // the float64 logs one block per lane, then their sum in block order (the same values and order as one lane
+    // summing log(rms) block by block)
+    for (int b = lane; b < nblk; b += 64) lg[b] = log((double)rms[b]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    double lsum = 0.0;
+    for (int b = 0; b < nblk; b++) lsum += lg[b];
     const float d = fmaxf(__half2float(__float2half((float)exp(lsum / (double)nblk))), 1e-8f);
     if (lane == 0) d_row[row] = d;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -161,11 +172,11 @@ extern "C" int ltq_row_scale(const float* w, long M, long K, long ldw, float sca
         return -1;
     const int nblk = (int)(K / 256);
     if (M == 0 || nblk == 0) return 0;
-    if (!w || !exp2_tab || !d_row || !e || !d || lde < nblk || ldd < nblk || ((uintptr_t)w & 15) || nblk > 4096)
+    if (!w || !exp2_tab || !d_row || !e || !d || lde < nblk || ldd < nblk || ((uintptr_t)w & 15) || nblk > 1024)
         return -1;
     const long grid = (M + 3) / 4;
-    hipLaunchKernelGGL(row_scale_kernel, dim3((unsigned)grid), dim3(256), 4 * 4 * nblk, (hipStream_t)stream, w, M, nblk,
-                       ldw, scale, (double)e_step, 1 << (e_bits - 1), exp2_tab, d_row, e, lde, d, ldd);
+    hipLaunchKernelGGL(row_scale_kernel, dim3((unsigned)grid), dim3(256), 4 * 12 * nblk, (hipStream_t)stream, w, M,
+                       nblk, ldw, scale, (double)e_step, 1 << (e_bits - 1), exp2_tab, d_row, e, lde, d, ldd);
     return (int)hipGetLastError();
 }
 
