@@ -49,11 +49,17 @@ __global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict_
     float* rms = (float*)(s_dyn + 4 * nblk) + wv * nblk;
     const float* wr = w + row * ldw;
     constexpr int kAhead = 8;  // blocks whose loads are in flight together
+    // rows start at different blocks (row * 13 mod nblk) so that the waves streaming their rows side by side do
+    // not all address the same offsets of equally spaced rows; each block's rms is independent of the order
+    const int rot = (int)((row * 13) % nblk);
     for (int b0 = 0; b0 < nblk; b0 += kAhead) {
         float4 v[kAhead];
 #pragma unroll
         for (int j = 0; j < kAhead; j++)
-            if (b0 + j < nblk) v[j] = *(const float4*)(wr + (b0 + j) * 256 + 4 * lane);
+            if (b0 + j < nblk) {
+                const int bj = b0 + j + rot < nblk ? b0 + j + rot : b0 + j + rot - nblk;
+                v[j] = *(const float4*)(wr + bj * 256 + 4 * lane);
+            }
         float s[kAhead];
 #pragma unroll
         for (int j = 0; j < kAhead; j++) s[j] = v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
@@ -65,7 +71,7 @@ __global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict_
         for (int j = 0; j < kAhead; j++) {
             if (b0 + j >= nblk) break;
             const float r = fmaxf(sqrtf(s[j] / 256.f), 1e-10f) * scale;
-            if (lane == 0) rms[b0 + j] = r;
+            if (lane == 0) rms[b0 + j + rot < nblk ? b0 + j + rot : b0 + j + rot - nblk] = r;
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
