@@ -205,6 +205,131 @@ __global__ __launch_bounds__(256) void pack_strip_kernel(const int16_t* __restri
     }
 }
 
+// Sub-blocks of 16 positions or more (every production format). One wavefront per 16 consecutive tiles of one
+// row group, no LDS and no barrier: lane (j = lane / 4, q = lane % 4) loads rows 4 q .. 4 q + 3 of tile j (four
+// 32-byte code runs and the gain index at each row's first position) and writes those rows' share of every
+// field. Each field stream is row-major with a fixed bit count per tile row (16 for codes and planes, 16 | 8 | 12
+// for lsb), so the share is a contiguous run of the tile's words and goes out as one 8 / 4 / 6-byte store; gains
+// (h bits per sub-block start) are assembled across the four lanes of the tile with quad broadcasts.
+// Bit gather: dword d of a row holds codes 2 d (low half) and 2 d + 1 (high half); rotating it right by
+// (b - 2 d) puts bit b of code 2 d at 2 d and of code 2 d + 1 at 16 + 2 d, so 8 rotate + mask-or steps collect
+// a row's even codes in the low half and odd codes in the high half, one shift interleaves them.
+__device__ inline uint32_t row_bits(const uint32_t (&x)[8], int b)
+{
+    uint32_t acc = 0;
+#pragma unroll
+    for (int d = 0; d < 8; d++)
+        acc |= __builtin_amdgcn_alignbit(x[d], x[d], (uint32_t)(b - 2 * d) & 31u) & (0x10001u << (2 * d));
+    return (acc & 0xffffu) | ((acc >> 15) & 0xfffeu);
+}
+
+// bit 0 of the first three codes of each quad (D4): code 4 m + k -> bit 3 m + k, 12 bits
+__device__ inline uint32_t row_lsb_d4(const uint32_t (&x)[8])
+{
+    uint32_t v = 0;
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+        v |= ((x[2 * m] & 1u) << (3 * m)) | (((x[2 * m] >> 16) & 1u) << (3 * m + 1)) | ((x[2 * m + 1] & 1u) << (3 * m + 2));
+    return v;
+}
+
+// bit 0 of the even codes (D2): code 2 d -> bit d, 8 bits
+__device__ inline uint32_t row_lsb_d2(const uint32_t (&x)[8])
+{
+    uint32_t v = 0;
+#pragma unroll
+    for (int d = 0; d < 8; d++) v |= (x[d] & 1u) << d;
+    return v;
+}
+
+template <int Q>
+__device__ inline uint32_t quad_lane(uint32_t v)  // lane Q of this lane's quad
+{
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, Q * 0x55, 0xf, 0xf, false);
+}
+
+__global__ __launch_bounds__(256) void pack_quads_kernel(const int16_t* __restrict__ idx, long ld_idx,
+                                                         const uint8_t* __restrict__ gi, long ld_gi, int R, int Kc,
+                                                         PackGeo g, int vec, uint8_t* __restrict__ out)
+{
+    const int lane = threadIdx.x & 63;
+    const int kbs = Kc / 16, spr = (kbs + 15) / 16;
+    const long T = (long)(R / 16) * kbs;
+    if (blockIdx.x == 0) {  // zero the gaps between regions (the reference pads with zero bytes)
+        for (int r = 1; r < 4; r++) {
+            const long end_prev = g.off[r - 1] + 2 * T * g.n[r - 1];
+            for (long b = end_prev + threadIdx.x; b < g.off[r]; b += blockDim.x) out[b] = 0;
+        }
+    }
+    const long wave = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wave >= (long)(R / 16) * spr) return;
+    const long rg = wave / spr;
+    const int kb = (int)(wave - rg * spr) * 16 + (lane >> 2);
+    if (kb >= kbs) return;  // whole quads leave together: the quad broadcasts below see four live lanes
+    const int q = lane & 3;
+    const long tile = rg * kbs + kb, row = rg * 16 + 4 * q, col = (long)kb * 16;
+    uint32_t x[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int16_t* src = idx + (row + i) * ld_idx + col;
+        if (vec) {
+            const uint4 a = *(const uint4*)src, b = *(const uint4*)(src + 8);
+            x[i][0] = a.x, x[i][1] = a.y, x[i][2] = a.z, x[i][3] = a.w;
+            x[i][4] = b.x, x[i][5] = b.y, x[i][6] = b.z, x[i][7] = b.w;
+        } else {
+#pragma unroll
+            for (int d = 0; d < 8; d++) x[i][d] = (uint32_t)(uint16_t)src[2 * d] | (uint32_t)(uint16_t)src[2 * d + 1] << 16;
+        }
+    }
+    const int rs = g.sub / 16;  // tile rows per sub-block
+    uint32_t gv = 0;            // this lane's gain bits, sub-block starts in row order
+    if (g.h) {
+        int k = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if ((4 * q + i) % rs == 0) gv |= ((uint32_t)gi[(row + i) * ld_gi + col] & ((1u << g.h) - 1)) << (g.h * k++);
+    }
+    // rows' words of one plane of bits: 4 words, rows 4 q .. 4 q + 3
+    auto put4 = [&](int f, long word, int b) {
+        const uint32_t w0 = row_bits(x[0], b) | row_bits(x[1], b) << 16, w1 = row_bits(x[2], b) | row_bits(x[3], b) << 16;
+        *(uint2*)(out + g.off[f] + 2 * word) = make_uint2(w0, w1);
+    };
+    put4(0, tile * 16 + 4 * q, g.K - 1);
+    for (int p = 1; p < g.K - 1; p++) put4(1, tile * g.n[1] + (p - 1) * 16 + 4 * q, p);
+    if (g.K > 1) {
+        if (g.frac == 0) {
+            put4(2, tile * 16 + 4 * q, 0);
+        } else if (g.frac == 1) {
+            const uint32_t v = row_lsb_d2(x[0]) | row_lsb_d2(x[1]) << 8 | row_lsb_d2(x[2]) << 16 | row_lsb_d2(x[3]) << 24;
+            *(uint32_t*)(out + g.off[2] + 2 * (tile * 8 + 2 * q)) = v;
+        } else {
+            const uint64_t v = (uint64_t)(row_lsb_d4(x[0]) | row_lsb_d4(x[1]) << 12) |
+                               (uint64_t)(row_lsb_d4(x[2]) | row_lsb_d4(x[3]) << 12) << 24;
+            uint16_t* dst = (uint16_t*)(out + g.off[2]) + tile * 12 + 3 * q;
+            dst[0] = (uint16_t)v;
+            dst[1] = (uint16_t)(v >> 16);
+            dst[2] = (uint16_t)(v >> 32);
+        }
+    }
+    if (g.h) {
+        // lane k's bits start after the sub-block starts of rows 0 .. 4 k - 1: ceil(4 k / rs) of them
+        const uint32_t v[4] = {quad_lane<0>(gv), quad_lane<1>(gv), quad_lane<2>(gv), quad_lane<3>(gv)};
+        uint64_t lo = 0, hi = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int o = (4 * k + rs - 1) / rs * g.h;
+            if (o < 64) {
+                lo |= (uint64_t)v[k] << o;
+                if (o > 32) hi |= (uint64_t)v[k] >> (64 - o);
+            } else {
+                hi |= (uint64_t)v[k] << (o - 64);
+            }
+        }
+        uint16_t* dst = (uint16_t*)(out + g.off[3]) + tile * g.n[3];
+        for (int w = q; w < g.n[3]; w += 4) dst[w] = (uint16_t)((w < 4 ? lo >> (16 * w) : hi >> (16 * (w - 4))) & 0xffff);
+    }
+}
+
 constexpr int kMaxRingWords = 512;  // codes 32 + planes <= 192 + lsb 32 + gains <= 256 for L <= 512
 
 // one wavefront per ring: record i = fields codes, planes, lsb, gains back to back (g.total bytes)
@@ -256,9 +381,16 @@ extern "C" int ltq_pack_slice(const int16_t* idx, long ld_idx, const uint8_t* gi
     const PackGeo g = pack_geo(R, K, fmt_K, frac, h, sub);
     if (g.n[0] + g.n[1] + g.n[2] + g.n[3] > kMaxTileWords) return -1;
     const long kbs = K / 16, spr = (kbs + kStrip - 1) / kStrip;
+    const int vec = ((uintptr_t)idx % 16 == 0) && ((uintptr_t)gi % 16 == 0) && ld_idx % 8 == 0 && ld_gi % 16 == 0;
+    if (sub >= 16) {  // 256 % sub == 0: at most one sub-block start per tile row
+        const long grid = ((long)(R / 16) * spr + 3) / 4;
+        if (grid > 0x7fffffffL) return -1;
+        hipLaunchKernelGGL(pack_quads_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, idx, ld_idx, gi,
+                           ld_gi, R, K, g, vec, out);
+        return (int)hipGetLastError();
+    }
     const long grid = (long)(R / 16) * spr;
     if (grid > 0x7fffffffL) return -1;
-    const int vec = ((uintptr_t)idx % 16 == 0) && ((uintptr_t)gi % 16 == 0) && ld_idx % 8 == 0 && ld_gi % 16 == 0;
     const size_t stage = (size_t)kStrip * (g.n[0] + g.n[1] + g.n[2] + g.n[3]) * sizeof(uint16_t);  // <= 8 KB
     hipLaunchKernelGGL(pack_strip_kernel, dim3((unsigned)grid), dim3(256), stage, (hipStream_t)stream, idx, ld_idx, gi,
                        ld_gi, R, K, g, vec, out);

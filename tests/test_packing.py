@@ -88,3 +88,28 @@ def test_gpu_quantize_pack_decode_roundtrip(name):
     dec = pack.decode_slice(b, R, K, f.K, f.frac, f.h, f.sub, f.masks, f.lut, f.gain_tab)
     rec_m = pack.untiles(rec.cpu().numpy(), R, K)
     assert np.array_equal(dec.view(np.uint32), rec_m.view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K,frac,h,sub", [(2, 1, 0, 32), (2, 0, 1, 16), (3, 2, 2, 16), (3, 1, 3, 32), (4, 0, 4, 64),
+                                          (5, 2, 8, 16), (8, 1, 5, 256), (6, 0, 7, 128), (3, 2, 2, 8), (4, 1, 3, 4)])
+@pytest.mark.parametrize("layout", ["contiguous", "strided"])
+def test_gpu_pack_random_slices(K, frac, h, sub, layout):
+    """Random codes and gain indices with bits above the format's (which packing ignores), 37 column blocks per
+    row group (two full 16-tile strips and a partial one), rows 16-byte aligned or on an odd stride (scalar loads):
+    the HIP packer writes the oracle's bytes for sub-blocks of 16 or more and for the smaller ones."""
+    from types import SimpleNamespace
+    from oracle import pack
+    from ltq_amd.ltq_file import pack_slice
+    f = SimpleNamespace(name=f"K{K}f{frac}h{h}s{sub}", K=K, frac=frac, h=h, sub=sub)
+    R, Kc = 48, 16 * 37
+    rng = np.random.default_rng(K * 1000 + frac * 100 + h * 10 + sub)
+    idx = rng.integers(0, 1 << 15, (R, Kc)).astype(np.int16)
+    gi = rng.integers(0, 256, (R, Kc)).astype(np.uint8)
+    ix_d, gi_d = torch.tensor(idx, device="cuda"), torch.tensor(gi, device="cuda")
+    if layout == "strided":
+        ix_d = torch.zeros((R, Kc + 3), dtype=torch.int16, device="cuda")[:, :Kc].copy_(ix_d)
+        gi_d = torch.zeros((R, Kc + 5), dtype=torch.uint8, device="cuda")[:, :Kc].copy_(gi_d)
+    print(f"pack random {f.name} {layout}", flush=True)
+    b = pack_slice(ix_d, gi_d, f)
+    assert np.array_equal(np.frombuffer(b, np.uint8), np.frombuffer(pack.pack_slice(idx, gi, K, frac, h, sub), np.uint8))
