@@ -54,7 +54,10 @@ __device__ __forceinline__ void fwht_wave(float v[4], int lane)
     for (int i = 0; i < 4; i++) v[i] *= 0.0625f;
 }
 
-// one wave per (row, 256-column block); SM: 0 none, 1 x / s[col], 2 x * s[col]
+// one wave per four consecutive (row, 256-column block) units, loads of all four issued before the first
+// transform; SM: 0 none, 1 x / s[col], 2 x * s[col]
+constexpr int kRowUnits = 4;
+
 template <int DT, int SM>
 __global__ __launch_bounds__(64 * kWaves) void fwht_rows_kernel(const void* __restrict__ x, float* __restrict__ y,
                                                                long rows, long nblk, long ldx, long ldy,
@@ -62,19 +65,31 @@ __global__ __launch_bounds__(64 * kWaves) void fwht_rows_kernel(const void* __re
 {
     const int lane = threadIdx.x & 63;
     const long total = rows * nblk;
-    for (long u = (long)blockIdx.x * kWaves + (threadIdx.x >> 6); u < total; u += (long)gridDim.x * kWaves) {
-        const long r = u / nblk, c = (u - r * nblk) * 256 + 4 * lane;
-        float v[4];
-        load4<DT>(x, r * ldx + c, v);
-        if constexpr (SM == 1) {
-            const float4 d = *(const float4*)(s + c);
-            v[0] = v[0] / d.x; v[1] = v[1] / d.y; v[2] = v[2] / d.z; v[3] = v[3] / d.w;
-        } else if constexpr (SM == 2) {
-            const float4 d = *(const float4*)(s + c);
-            v[0] = v[0] * d.x; v[1] = v[1] * d.y; v[2] = v[2] * d.z; v[3] = v[3] * d.w;
+    const long stride = (long)gridDim.x * kWaves * kRowUnits;
+    for (long u0 = ((long)blockIdx.x * kWaves + (threadIdx.x >> 6)) * kRowUnits; u0 < total; u0 += stride) {
+        float v[kRowUnits][4];
+        long r[kRowUnits], c[kRowUnits];
+#pragma unroll
+        for (int j = 0; j < kRowUnits; j++) {
+            const long u = u0 + j < total ? u0 + j : total - 1;  // a short last group repeats its last unit
+            r[j] = u / nblk;
+            c[j] = (u - r[j] * nblk) * 256 + 4 * lane;
+            load4<DT>(x, r[j] * ldx + c[j], v[j]);
         }
-        fwht_wave(v, lane);
-        *(float4*)(y + r * ldy + c) = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+        for (int j = 0; j < kRowUnits; j++) {
+            if constexpr (SM == 1) {
+                const float4 d = *(const float4*)(s + c[j]);
+                v[j][0] = v[j][0] / d.x; v[j][1] = v[j][1] / d.y; v[j][2] = v[j][2] / d.z; v[j][3] = v[j][3] / d.w;
+            } else if constexpr (SM == 2) {
+                const float4 d = *(const float4*)(s + c[j]);
+                v[j][0] = v[j][0] * d.x; v[j][1] = v[j][1] * d.y; v[j][2] = v[j][2] * d.z; v[j][3] = v[j][3] * d.w;
+            }
+            fwht_wave(v[j], lane);
+        }
+#pragma unroll
+        for (int j = 0; j < kRowUnits; j++)
+            if (u0 + j < total) *(float4*)(y + r[j] * ldy + c[j]) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
     }
 }
 
@@ -86,10 +101,10 @@ __global__ __launch_bounds__(64 * kWaves) void fwht_rows_kernel(const void* __re
 // before the transform.
 constexpr int kColTile = 64;
 
-template <int SM>
+template <int SM, bool VEC>
 __global__ __launch_bounds__(64 * kWaves) void fwht_cols_kernel(const float* __restrict__ x, float* __restrict__ y,
                                                                long rows, long cols, long ldx, long ldy,
-                                                               const float* __restrict__ s, int vec)
+                                                               const float* __restrict__ s)
 {
     __shared__ __align__(16) float t[256][kColTile];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -98,27 +113,33 @@ __global__ __launch_bounds__(64 * kWaves) void fwht_cols_kernel(const float* __r
     const int c4 = 4 * (tid & 15), i0 = tid >> 4;  // rows i0 + 16 k, columns c4 .. c4 + 3
     for (long u = blockIdx.x; u < total; u += gridDim.x) {
         const long r0 = (u / ctiles) * 256, cg = (u % ctiles) * kColTile + c4;
-        for (int k = 0; k < 16; k++) {
-            const long row = r0 + i0 + 16 * k;
-            float4 f;
-            if (vec && cg + 3 < cols) {
-                f = *(const float4*)(x + row * ldx + cg);
-            } else {
-                float v[4];
+        float4 f[16];  // all 16 row segments in flight before the first LDS store
+        if (VEC) {
 #pragma unroll
-                for (int e = 0; e < 4; e++) v[e] = cg + e < cols ? x[row * ldx + cg + e] : 0.f;
-                f = make_float4(v[0], v[1], v[2], v[3]);
+            for (int k = 0; k < 16; k++) f[k] = *(const float4*)(x + (r0 + i0 + 16 * k) * ldx + cg);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const float* src = x + (r0 + i0 + 16 * k) * ldx + cg;
+                f[k] = make_float4(cg < cols ? src[0] : 0.f, cg + 1 < cols ? src[1] : 0.f, cg + 2 < cols ? src[2] : 0.f,
+                                   cg + 3 < cols ? src[3] : 0.f);
             }
-            if constexpr (SM != 0) {
-                const float sr = s[row];
+        }
+        if constexpr (SM != 0) {
+            float sr[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) sr[k] = s[r0 + i0 + 16 * k];
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
                 if constexpr (SM == 1) {
-                    f.x = f.x / sr; f.y = f.y / sr; f.z = f.z / sr; f.w = f.w / sr;
+                    f[k].x = f[k].x / sr[k]; f[k].y = f[k].y / sr[k]; f[k].z = f[k].z / sr[k]; f[k].w = f[k].w / sr[k];
                 } else {
-                    f.x = f.x * sr; f.y = f.y * sr; f.z = f.z * sr; f.w = f.w * sr;
+                    f[k].x = f[k].x * sr[k]; f[k].y = f[k].y * sr[k]; f[k].z = f[k].z * sr[k]; f[k].w = f[k].w * sr[k];
                 }
             }
-            *(float4*)&t[i0 + 16 * k][c4] = f;
         }
+#pragma unroll
+        for (int k = 0; k < 16; k++) *(float4*)&t[i0 + 16 * k][c4] = f[k];
         __syncthreads();
         // pass 1: wave w, row groups 4 w .. 4 w + 3 of 16 consecutive rows; stages h = 1, 2, 4, 8
         for (int gq = 0; gq < 4; gq++) {
@@ -158,16 +179,17 @@ __global__ __launch_bounds__(64 * kWaves) void fwht_cols_kernel(const float* __r
             for (int k = 0; k < 16; k++) t[rl + 16 * k][lane] = v[k] * 0.0625f;
         }
         __syncthreads();
-        for (int k = 0; k < 16; k++) {
-            const long row = r0 + i0 + 16 * k;
-            const float4 f = *(const float4*)&t[i0 + 16 * k][c4];
-            if (vec && cg + 3 < cols) {
-                *(float4*)(y + row * ldy + cg) = f;
-            } else {
-                const float v[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (cg + e < cols) y[row * ldy + cg + e] = v[e];
+        for (int k = 0; k < 16; k++) {
+            const float4 o = *(const float4*)&t[i0 + 16 * k][c4];
+            float* dst = y + (r0 + i0 + 16 * k) * ldy + cg;
+            if (VEC) {
+                *(float4*)dst = o;
+            } else {
+                if (cg < cols) dst[0] = o.x;
+                if (cg + 1 < cols) dst[1] = o.y;
+                if (cg + 2 < cols) dst[2] = o.z;
+                if (cg + 3 < cols) dst[3] = o.w;
             }
         }
         __syncthreads();
@@ -192,11 +214,23 @@ int rows_dispatch(const void* x, float* y, long rows, long cols, long ldx, long 
                   hipStream_t st)
 {
     const long nblk = cols / 256;
-    const int grid = grid_for(rows * nblk);
+    const int grid = grid_for((rows * nblk + kRowUnits - 1) / kRowUnits);
     switch (smode) {
         case 0: hipLaunchKernelGGL((fwht_rows_kernel<DT, 0>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, nblk, ldx, ldy, s); break;
         case 1: hipLaunchKernelGGL((fwht_rows_kernel<DT, 1>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, nblk, ldx, ldy, s); break;
         default: hipLaunchKernelGGL((fwht_rows_kernel<DT, 2>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, nblk, ldx, ldy, s); break;
+    }
+    return (int)hipGetLastError();
+}
+
+template <bool VEC>
+int cols_dispatch(const float* x, float* y, long rows, long cols, long ldx, long ldy, const float* s, int smode,
+                  int grid, hipStream_t st)
+{
+    switch (smode) {
+        case 0: hipLaunchKernelGGL((fwht_cols_kernel<0, VEC>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s); break;
+        case 1: hipLaunchKernelGGL((fwht_cols_kernel<1, VEC>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s); break;
+        default: hipLaunchKernelGGL((fwht_cols_kernel<2, VEC>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s); break;
     }
     return (int)hipGetLastError();
 }
@@ -228,11 +262,9 @@ extern "C" int ltq_fwht256_cols(const float* x, float* y, long rows, long cols, 
     hipStream_t st = (hipStream_t)stream;
     const long tiles = (rows / 256) * ((cols + kColTile - 1) / kColTile);
     const int grid = grid_for(tiles * kWaves);
-    const int vec = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && ldx % 4 == 0 && ldy % 4 == 0;
-    switch (smode) {
-        case 0: hipLaunchKernelGGL((fwht_cols_kernel<0>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s, vec); break;
-        case 1: hipLaunchKernelGGL((fwht_cols_kernel<1>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s, vec); break;
-        default: hipLaunchKernelGGL((fwht_cols_kernel<2>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s, vec); break;
-    }
-    return (int)hipGetLastError();
+    // whole float4 row segments: aligned rows and every 64-column tile full
+    const bool vec = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && ldx % 4 == 0 && ldy % 4 == 0 &&
+                     cols % kColTile == 0;
+    if (vec) return cols_dispatch<true>(x, y, rows, cols, ldx, ldy, s, smode, grid, st);
+    return cols_dispatch<false>(x, y, rows, cols, ldx, ldy, s, smode, grid, st);
 }

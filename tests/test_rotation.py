@@ -95,7 +95,7 @@ def test_gpu_fwht_rows_fused_scale(oracle, dtype, mode):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("cols", [32, 77, 300])
+@pytest.mark.parametrize("cols", [32, 77, 128, 300, 448])
 @pytest.mark.parametrize("mode", [0, 2])
 def test_gpu_fwht_cols_matches_transposed_rows(oracle, cols, mode):
     """fwht_cols(x, s) == fwht_inplace(x.T * s).T of the reference (the second side of H, liqk_v2.py:440)."""
