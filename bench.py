@@ -280,8 +280,11 @@ class DeviceEvent:
 
 
 class KernelTimer:
-    """HIP events around the calls of selected product functions inside the timed steps, on the current stream
-    (the stream the kernels are launched on). Each record is (name, start, end, algorithmic bytes, flops)."""
+    """Kernel times of selected product calls inside the timed steps. Each wrapped call launches one library
+    kernel; the call arms ltq_kernel_timing with a start / stop DeviceEvent pair, so that launch carries the
+    events (hipExtLaunchKernelGGL stamps them with the dispatch's own start and end: no marker packets around
+    the kernel, no allocator or host work inside the interval). Each record is (name, start, end, algorithmic
+    bytes, flops)."""
 
     def __init__(self):
         self.records = []
@@ -289,17 +292,19 @@ class KernelTimer:
         self._undo = []
 
     def _wrap(self, owner, attr, name_fn):
-        import torch
+        from ltq_amd import _lib
+        lib = _lib.lib()
         orig = getattr(owner, attr)
 
         def timed(*a, **k):
             if not self.active:
                 return orig(*a, **k)
-            st = torch.cuda.current_stream()
             e0, e1 = DeviceEvent(), DeviceEvent()
-            e0.record(st)
-            out = orig(*a, **k)
-            e1.record(st)
+            lib.ltq_kernel_timing(e0.handle, e1.handle, 1)
+            try:
+                out = orig(*a, **k)
+            finally:
+                lib.ltq_kernel_timing(None, None, 0)
             name, nbytes, flops = name_fn(a, k, out)
             if name:
                 self.records.append((name, e0, e1, nbytes, flops))

@@ -53,6 +53,12 @@ long tcq_viterbi_static_bytes(void);
  * affected. */
 int ltq_viterbi_timing(void* start_event, void* stop_event, int launches);
 
+/* The same hook for the library's other kernels (no counterpart in the reference): the next `launches` launches
+ * of ltq_fwht256_rows / ltq_fwht256_cols, ltq_row_scale, ltq_pack_slice / ltq_pack_rings and ltq_ldlq_err /
+ * ltq_ldlq_update on the calling host thread carry start_event (first) and stop_event (last). Each of those
+ * entry points launches one kernel. launches = 0 disarms. Returns 0, or -1 for launches < 0. */
+int ltq_kernel_timing(void* start_event, void* stop_event, int launches);
+
 /* LUT sub-block quantization of the diagonal profile: for S sub-blocks of 16 weights xs[S, 16] with weights
  * dh[S, 16], bucket b = clamp(rint(x * inv_step + half_b), 0, nb - 1) picks a row of 64 candidates of lut[nb, 64];
  * the first candidate with the lowest sum_j dh (xs - lut[b_j][c])^2 gives out[S, 16] = lut[b_j][c]. Same

@@ -12,6 +12,7 @@
 #include <stdint.h>
 
 #include "ltq_hip.h"
+#include "ltq_timing.h"
 
 namespace {
 
@@ -214,25 +215,22 @@ int rows_dispatch(const void* x, float* y, long rows, long cols, long ldx, long 
                   hipStream_t st)
 {
     const long nblk = cols / 256;
-    const int grid = grid_for((rows * nblk + kRowUnits - 1) / kRowUnits);
-    switch (smode) {
-        case 0: hipLaunchKernelGGL((fwht_rows_kernel<DT, 0>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, nblk, ldx, ldy, s); break;
-        case 1: hipLaunchKernelGGL((fwht_rows_kernel<DT, 1>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, nblk, ldx, ldy, s); break;
-        default: hipLaunchKernelGGL((fwht_rows_kernel<DT, 2>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, nblk, ldx, ldy, s); break;
-    }
-    return (int)hipGetLastError();
+    const dim3 grid(grid_for((rows * nblk + kRowUnits - 1) / kRowUnits)), block(64 * kWaves);
+    auto& hook = ltq::kernel_timing;
+    if (smode == 0) return ltq::timed_launch(hook, fwht_rows_kernel<DT, 0>, grid, block, 0, st, x, y, rows, nblk, ldx, ldy, s);
+    if (smode == 1) return ltq::timed_launch(hook, fwht_rows_kernel<DT, 1>, grid, block, 0, st, x, y, rows, nblk, ldx, ldy, s);
+    return ltq::timed_launch(hook, fwht_rows_kernel<DT, 2>, grid, block, 0, st, x, y, rows, nblk, ldx, ldy, s);
 }
 
 template <bool VEC>
 int cols_dispatch(const float* x, float* y, long rows, long cols, long ldx, long ldy, const float* s, int smode,
                   int grid, hipStream_t st)
 {
-    switch (smode) {
-        case 0: hipLaunchKernelGGL((fwht_cols_kernel<0, VEC>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s); break;
-        case 1: hipLaunchKernelGGL((fwht_cols_kernel<1, VEC>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s); break;
-        default: hipLaunchKernelGGL((fwht_cols_kernel<2, VEC>), dim3(grid), dim3(64 * kWaves), 0, st, x, y, rows, cols, ldx, ldy, s); break;
-    }
-    return (int)hipGetLastError();
+    const dim3 g(grid), block(64 * kWaves);
+    auto& hook = ltq::kernel_timing;
+    if (smode == 0) return ltq::timed_launch(hook, fwht_cols_kernel<0, VEC>, g, block, 0, st, x, y, rows, cols, ldx, ldy, s);
+    if (smode == 1) return ltq::timed_launch(hook, fwht_cols_kernel<1, VEC>, g, block, 0, st, x, y, rows, cols, ldx, ldy, s);
+    return ltq::timed_launch(hook, fwht_cols_kernel<2, VEC>, g, block, 0, st, x, y, rows, cols, ldx, ldy, s);
 }
 
 }  // namespace

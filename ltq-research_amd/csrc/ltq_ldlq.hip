@@ -32,6 +32,7 @@
 #include <stdint.h>
 
 #include "ltq_hip.h"
+#include "ltq_timing.h"
 
 namespace {
 
@@ -181,9 +182,9 @@ extern "C" int ltq_row_scale(const float* w, long M, long K, long ldw, float sca
     if (!w || !exp2_tab || !d_row || !e || !d || lde < nblk || ldd < nblk || ((uintptr_t)w & 15) || nblk > 1024)
         return -1;
     const long grid = (M + 3) / 4;
-    hipLaunchKernelGGL(row_scale_kernel, dim3((unsigned)grid), dim3(256), 4 * 12 * nblk, (hipStream_t)stream, w, M,
-                       nblk, ldw, scale, (double)e_step, 1 << (e_bits - 1), exp2_tab, d_row, e, lde, d, ldd);
-    return (int)hipGetLastError();
+    return ltq::timed_launch(ltq::kernel_timing, row_scale_kernel, dim3((unsigned)grid), dim3(256),
+                             (uint32_t)(4 * 12 * nblk), (hipStream_t)stream, w, M, nblk, ldw, scale, (double)e_step,
+                             1 << (e_bits - 1), exp2_tab, d_row, e, lde, d, ldd);
 }
 
 extern "C" int ltq_ldlq_prep(const float* wk, long ldw, const float* d, long ldd, float* x, long M, void* stream)

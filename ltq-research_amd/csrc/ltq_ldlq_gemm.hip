@@ -25,6 +25,7 @@
 #include <stdint.h>
 
 #include "ltq_hip.h"
+#include "ltq_timing.h"
 
 namespace {
 
@@ -194,13 +195,9 @@ int launch_gemm(int amode, int epi, GemmArgs p, hipStream_t st)
     p.tiles_n = (int)(p.N / BN);
     const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
     if (grid == 0) return 0;
-    if (amode == 0 && epi == 1)
-        hipLaunchKernelGGL((ldlq_gemm_kernel<0, 1>), dim3(grid), dim3(256), 0, st, p);
-    else if (amode == 1 && epi == 0)
-        hipLaunchKernelGGL((ldlq_gemm_kernel<1, 0>), dim3(grid), dim3(256), 0, st, p);
-    else
-        return -1;
-    return (int)hipGetLastError();
+    if (amode == 0 && epi == 1) return ltq::timed_launch(ltq::kernel_timing, ldlq_gemm_kernel<0, 1>, dim3(grid), dim3(256), 0, st, p);
+    if (amode == 1 && epi == 0) return ltq::timed_launch(ltq::kernel_timing, ldlq_gemm_kernel<1, 0>, dim3(grid), dim3(256), 0, st, p);
+    return -1;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }

@@ -19,6 +19,7 @@
 #include <stdint.h>
 
 #include "ltq_hip.h"
+#include "ltq_timing.h"
 
 namespace {
 
@@ -385,16 +386,14 @@ extern "C" int ltq_pack_slice(const int16_t* idx, long ld_idx, const uint8_t* gi
     if (sub >= 16) {  // 256 % sub == 0: at most one sub-block start per tile row
         const long grid = ((long)(R / 16) * spr + 3) / 4;
         if (grid > 0x7fffffffL) return -1;
-        hipLaunchKernelGGL(pack_quads_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, idx, ld_idx, gi,
-                           ld_gi, R, K, g, vec, out);
-        return (int)hipGetLastError();
+        return ltq::timed_launch(ltq::kernel_timing, pack_quads_kernel, dim3((unsigned)grid), dim3(256), 0,
+                                 (hipStream_t)stream, idx, ld_idx, gi, ld_gi, R, K, g, vec, out);
     }
     const long grid = (long)(R / 16) * spr;
     if (grid > 0x7fffffffL) return -1;
     const size_t stage = (size_t)kStrip * (g.n[0] + g.n[1] + g.n[2] + g.n[3]) * sizeof(uint16_t);  // <= 8 KB
-    hipLaunchKernelGGL(pack_strip_kernel, dim3((unsigned)grid), dim3(256), stage, (hipStream_t)stream, idx, ld_idx, gi,
-                       ld_gi, R, K, g, vec, out);
-    return (int)hipGetLastError();
+    return ltq::timed_launch(ltq::kernel_timing, pack_strip_kernel, dim3((unsigned)grid), dim3(256), (uint32_t)stage,
+                             (hipStream_t)stream, idx, ld_idx, gi, ld_gi, R, K, g, vec, out);
 }
 
 extern "C" long ltq_ring_bytes(int L, int fmt_K, int frac, int h, int sub)
@@ -414,9 +413,8 @@ extern "C" int ltq_pack_rings(const int16_t* idx, long ld_idx, const uint8_t* gi
     if (g.n[0] + g.n[1] + g.n[2] + g.n[3] > kMaxRingWords) return -1;
     long grid = (n_rings + kWaves - 1) / kWaves;
     if (grid > 65536) grid = 65536;
-    hipLaunchKernelGGL(pack_rings_kernel, dim3((unsigned)grid), dim3(64 * kWaves), 0, (hipStream_t)stream, idx, ld_idx, gi,
-                       ld_gi, n_rings, g, out);
-    return (int)hipGetLastError();
+    return ltq::timed_launch(ltq::kernel_timing, pack_rings_kernel, dim3((unsigned)grid), dim3(64 * kWaves), 0,
+                             (hipStream_t)stream, idx, ld_idx, gi, ld_gi, n_rings, g, out);
 }
 
 // ---- decoding (src/ltq_file.py:119-147, the spec decoder) ------------------------------------------------

@@ -1,0 +1,13 @@
+// Instantiations of the Viterbi launcher for parity mode 0, radix block 3 (S = 1024, 8 states per lane, G = 8; every
+// label count). Split by radix block so the units compile in parallel.
+#include "tcq_launch.h"
+namespace ltq {
+template int launch<10, 3, 0, 4>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 3, 0, 4>(const TcqArgs&, const TcqArgs&, hipStream_t);
+template int launch<10, 3, 0, 8>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 3, 0, 8>(const TcqArgs&, const TcqArgs&, hipStream_t);
+template int launch<10, 3, 0, 16>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 3, 0, 16>(const TcqArgs&, const TcqArgs&, hipStream_t);
+template int launch<10, 3, 0, 32>(const TcqArgs&, hipStream_t);
+template int launch_tb<10, 3, 0, 32>(const TcqArgs&, const TcqArgs&, hipStream_t);
+}  // namespace ltq

@@ -5,14 +5,10 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include "ltq_timing.h"
 #include "tcq_trellis.h"
 
 namespace ltq {
-
-// Timing hook (ltq_viterbi_timing): the start / stop events the next Viterbi launch of this thread carries, or
-// null. Launches with an event go through hipExtLaunchKernelGGL, which stamps the events with the dispatch's
-// own start and end times (no event packet between two kernels).
-void timing_take(hipEvent_t* start, hipEvent_t* stop);
 
 extern "C" __shared__ __align__(16) char ltq_dyn_smem[];
 
@@ -164,7 +160,7 @@ int launch(const TcqArgs& a, hipStream_t stream)
             if (const int e = set_max_lds_once(tcq_viterbi_kernel<NU, RB, MD, NL, 8>, half, attr2)) return e;
             const int threads = 64 * a.G * Geo<NU, RB>::Q;
             hipEvent_t e0 = nullptr, e1 = nullptr;
-            timing_take(&e0, &e1);
+            viterbi_timing.take(&e0, &e1);
             hipExtLaunchKernelGGL((tcq_viterbi_kernel<NU, RB, MD, NL, 8>), dim3(a.N), dim3(threads), H.total, stream,
                                   e0, e1, 0, a, half);
             return 0;
@@ -176,7 +172,7 @@ int launch(const TcqArgs& a, hipStream_t stream)
     if (const int e = set_max_lds_once(tcq_viterbi_kernel<NU, RB, MD, NL>, lds_max, attr)) return e;
     const int threads = 64 * a.G * Geo<NU, RB>::Q;
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    timing_take(&e0, &e1);
+    viterbi_timing.take(&e0, &e1);
     hipExtLaunchKernelGGL((tcq_viterbi_kernel<NU, RB, MD, NL>), dim3(a.N), dim3(threads), L.total, stream, e0, e1, 0,
                           a, lds_max);
     return 0;
@@ -195,7 +191,7 @@ int launch_tb(const TcqArgs& a1, const TcqArgs& a2, hipStream_t stream)
     if (const int e = set_max_lds_once(tcq_viterbi_tb_kernel<NU, RB, MD, NL>, lds_max, attr)) return e;
     const int threads = 64 * a2.G * Geo<NU, RB>::Q;
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    timing_take(&e0, &e1);
+    viterbi_timing.take(&e0, &e1);
     hipExtLaunchKernelGGL((tcq_viterbi_tb_kernel<NU, RB, MD, NL>), dim3(a2.N), dim3(threads), total, stream, e0, e1,
                           0, a1, a2, lds_max);
     return 0;

@@ -10,6 +10,7 @@
 
 #include <mutex>
 
+#include "ltq_timing.h"
 #include "tcq_launch.h"
 
 #include "ltq_hip.h"
@@ -27,27 +28,6 @@ LTQ_EXT(8, 2, 0, 4)
 LTQ_EXT_MD(0) LTQ_EXT_MD(1) LTQ_EXT_MD(2) LTQ_EXT_MD(3)
 #undef LTQ_EXT_MD
 #undef LTQ_EXT
-
-// timing hook: armed by ltq_viterbi_timing, consumed launch by launch on the arming thread
-namespace {
-struct Timing {
-    hipEvent_t start = nullptr, stop = nullptr;
-    int left = 0;  // launches still to go; the last one carries stop
-};
-thread_local Timing t_timing;
-}  // namespace
-
-void timing_take(hipEvent_t* start, hipEvent_t* stop)
-{
-    Timing& t = t_timing;
-    if (t.left <= 0) return;
-    *start = t.start;
-    t.start = nullptr;
-    if (--t.left == 0) {
-        *stop = t.stop;
-        t.stop = nullptr;
-    }
-}
 
 // per-device attributes of the current device, cached per device ordinal (a process may drive several GPUs)
 constexpr int kMaxDevices = 64;
@@ -221,9 +201,13 @@ extern "C" int tcq_viterbi_static(const float* x, const float* w, const float* t
 extern "C" int ltq_viterbi_timing(void* start_event, void* stop_event, int launches)
 {
     if (launches < 0) return -1;
-    ltq::Timing& t = ltq::t_timing;
-    t.start = (hipEvent_t)start_event;
-    t.stop = (hipEvent_t)stop_event;
-    t.left = launches;
+    ltq::viterbi_timing.arm((hipEvent_t)start_event, (hipEvent_t)stop_event, launches);
+    return 0;
+}
+
+extern "C" int ltq_kernel_timing(void* start_event, void* stop_event, int launches)
+{
+    if (launches < 0) return -1;
+    ltq::kernel_timing.arm((hipEvent_t)start_event, (hipEvent_t)stop_event, launches);
     return 0;
 }

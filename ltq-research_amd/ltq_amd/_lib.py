@@ -24,6 +24,7 @@ SIGNATURES = {
     "tcq_viterbi_static_bytes": (cl, []),
     # timing hook for benchmarks (no reference counterpart): start / stop HIP events carried by the next launches
     "ltq_viterbi_timing": (ci, [vp, vp, ci]),
+    "ltq_kernel_timing": (ci, [vp, vp, ci]),
     # src/cuda/tcq_viterbi.cu:806-807; src/tcq_proto.py:531-532
     "lut_subs_quant": (ci, [vp] * 4 + [ci, cf, cf, ci, vp]),
     # FWHT-256 (src/iqk_format.py:153-170), rows with a fused scale / columns

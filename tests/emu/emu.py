@@ -5,6 +5,8 @@ Same argument convention as the reference ABI tcq_viterbi (src/cuda/tcq_viterbi.
 from __future__ import annotations
 
 import ctypes
+import fcntl
+import os
 import subprocess
 from pathlib import Path
 
@@ -15,12 +17,19 @@ _LIB = {}
 
 
 def build(asan: bool = False) -> Path:
+    """Compile the emulator library; written under a temporary name and renamed, so a concurrent loader never
+    maps a half-written file."""
     so = _DIR / ("libtcq_emu_asan.so" if asan else "libtcq_emu.so")
+    tmp = so.with_name(f"{so.name}.{os.getpid()}.tmp")
     cmd = ["g++", "-std=c++20", "-O1" if asan else "-O2", "-g", "-fPIC", "-shared", "-ffp-contract=off",
-           "-fno-fast-math", "-pthread", "-o", str(so), str(_DIR / "tcq_emu.cpp")]
+           "-fno-fast-math", "-pthread", "-o", str(tmp), str(_DIR / "tcq_emu.cpp")]
     if asan:
         cmd.insert(1, "-fsanitize=address")
-    subprocess.run(cmd, check=True)
+    try:
+        subprocess.run(cmd, check=True)
+        os.replace(tmp, so)
+    finally:
+        tmp.unlink(missing_ok=True)
     return so
 
 
@@ -28,8 +37,10 @@ def lib(asan: bool = False):
     if asan not in _LIB:
         so = _DIR / ("libtcq_emu_asan.so" if asan else "libtcq_emu.so")
         srcs = (_DIR / "tcq_emu.cpp", _DIR.parent.parent / "ltq-research_amd" / "csrc" / "tcq_trellis.h")
-        if not so.exists() or so.stat().st_mtime < max(f.stat().st_mtime for f in srcs):
-            build(asan)  # missing, or older than the kernel body it emulates
+        with open(_DIR / ".build.lock", "w") as lk:  # one rebuild among parallel test workers
+            fcntl.flock(lk, fcntl.LOCK_EX)
+            if not so.exists() or so.stat().st_mtime < max(f.stat().st_mtime for f in srcs):
+                build(asan)  # missing, or older than the kernel body it emulates
         L = ctypes.CDLL(str(so))
         L.tcq_viterbi_emu.restype = ctypes.c_int
         L.tcq_viterbi_emu.argtypes = [ctypes.c_void_p] * 15 + [ctypes.c_int] * 18 + [ctypes.c_void_p, ctypes.c_int]

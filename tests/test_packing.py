@@ -113,3 +113,34 @@ def test_gpu_pack_random_slices(K, frac, h, sub, layout):
     print(f"pack random {f.name} {layout}", flush=True)
     b = pack_slice(ix_d, gi_d, f)
     assert np.array_equal(np.frombuffer(b, np.uint8), np.frombuffer(pack.pack_slice(idx, gi, K, frac, h, sub), np.uint8))
+
+
+@pytest.mark.gpu
+def test_gpu_kernel_timing_hook_keeps_results():
+    """ltq_kernel_timing hands a start / stop event pair to the next pack launch (the benchmark's HBM timing):
+    the packed bytes are unchanged, both events are stamped, and the hook is spent after that one launch."""
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+    import bench
+    from ltq_amd import _lib
+    from ltq_amd.formats import make_format
+    from ltq_amd.ltq_file import pack_slice_device
+    f = make_format("TCQ275X2")
+    rng = np.random.default_rng(9)
+    idx = torch.tensor(rng.integers(0, 1 << 15, (64, 1024)).astype(np.int16), device="cuda")
+    gi = torch.tensor(rng.integers(0, 4, (64, 1024)).astype(np.uint8), device="cuda")
+    ref = pack_slice_device(idx, gi, f)
+    e0, e1 = bench.DeviceEvent(), bench.DeviceEvent()
+    assert _lib.lib().ltq_kernel_timing(e0.handle, e1.handle, 1) == 0
+    try:
+        out = pack_slice_device(idx, gi, f)
+    finally:
+        _lib.lib().ltq_kernel_timing(None, None, 0)
+    again = pack_slice_device(idx, gi, f)
+    torch.cuda.synchronize()
+    assert torch.equal(ref, out) and torch.equal(ref, again)
+    ms = e0.elapsed_time(e1)
+    print(f"pack of 256 tiles: {ms * 1e3:.1f} us", flush=True)
+    assert 0.0 < ms < 50.0
+    assert _lib.lib().ltq_kernel_timing(None, None, -1) == -1
