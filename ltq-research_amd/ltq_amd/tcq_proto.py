@@ -13,43 +13,55 @@ import torch
 
 from . import _lib
 
-# timing hook (off by default): a list receives one record per sampled call -- a tail-biting call (its two
-# passes back to back between one pair of events) or a single pass -- for calls 0, LAUNCH_SAMPLE,
-# 2 LAUNCH_SAMPLE, ... counted from the last reset of _launch_count. A record is a dict: "ev" (start, end)
-# torch.cuda.Event recorded on the stream the kernels run on, "tiles", "launches" ((steps, gain slots run) of
-# each pass between the events), "pp" (parity mode).
+# timing hook (off by default): a list receives one record per sampled call -- a tail-biting call (both passes)
+# or a single pass -- for calls 0, LAUNCH_SAMPLE, 2 LAUNCH_SAMPLE, ... counted from the last reset of
+# _launch_count. A record is a dict: "ev" a list of (start, end) event pairs, "tiles", "launches" ((steps, gain
+# slots run) of each pass), "pp" (parity mode).
 LAUNCH_EVENTS: list | None = None
 LAUNCH_SAMPLE = 1
 _launch_count = 0
-# the hook's event type: a callable returning an object with record(stream) and elapsed_time(end) in ms
-# (torch.cuda.Event with timing when None). An object with a `handle` (its hipEvent_t) is not recorded around
-# the call but handed to the kernel launches themselves (ltq_viterbi_timing): the first launch of the call
-# stamps the start event with its dispatch start, the last one the stop event with its end.
+# the hook's event type: None for torch.cuda.Event, one pair recorded on the stream around the whole call; or
+# a callable returning an object with `handle` (its hipEvent_t) and elapsed_time(end) in ms, handed to the kernel
+# launch itself (ltq_viterbi_timing), which stamps it with the dispatch's own start / end: each kernel launch of
+# the call then gets its own pair, so the record holds the kernels' durations and not the dispatch gap between
+# two dependent launches.
 EVENT_FACTORY = None
+_PER_LAUNCH: list | None = None  # pairs of the launches of the sampled call in progress
 
 
-def _timed_call(fn, tiles, launches, pp):
-    """fn() between two events when the timing hook samples this call."""
-    global _launch_count
+def _timed_call(fn, tiles, launches, pp, kernels=None):
+    """fn() with timing events when the timing hook samples this call. kernels=1: fn issues one kernel launch
+    (inside a sampled composite call it then takes its own event pair)."""
+    global _launch_count, _PER_LAUNCH
+    if _PER_LAUNCH is not None and kernels == 1:
+        e0, e1 = EVENT_FACTORY(), EVENT_FACTORY()
+        _lib.lib().ltq_viterbi_timing(e0.handle, e1.handle, 1)
+        try:
+            out = fn()
+        finally:
+            _lib.lib().ltq_viterbi_timing(None, None, 0)
+        _PER_LAUNCH.append((e0, e1))
+        return out
     take = LAUNCH_EVENTS is not None and _launch_count % LAUNCH_SAMPLE == 0
     if LAUNCH_EVENTS is not None:
         _launch_count += 1
     if not take:
         return fn()
-    st = torch.cuda.current_stream()
-    mk = EVENT_FACTORY or (lambda: torch.cuda.Event(enable_timing=True))
-    e0, e1 = mk(), mk()
-    if hasattr(e0, "handle"):
-        _lib.lib().ltq_viterbi_timing(e0.handle, e1.handle, len(launches))
+    if EVENT_FACTORY is not None:
+        _PER_LAUNCH = []
         try:
-            out = fn()
+            out = _timed_call(fn, tiles, launches, pp, kernels) if kernels == 1 else fn()
+            pairs = _PER_LAUNCH
         finally:
-            _lib.lib().ltq_viterbi_timing(None, None, 0)
+            _PER_LAUNCH = None
     else:
+        st = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(st)
         out = fn()
         e1.record(st)
-    LAUNCH_EVENTS.append({"ev": (e0, e1), "tiles": tiles, "launches": launches, "pp": pp})
+        pairs = [(e0, e1)]
+    LAUNCH_EVENTS.append({"ev": pairs, "tiles": tiles, "launches": launches, "pp": pp})
     return out
 
 
@@ -198,7 +210,7 @@ def viterbi_ub_cuda(x: torch.Tensor, small: torch.Tensor, K: int, nu: int, m: in
                                       Gfull, m, sub, tab_hi.numel() // nl, mix_arg, me[0], me[1], me[2], nl, ld, _rot,
                                       p(pbits), pp, _lib.stream_ptr())
 
-    rc = _timed_call(launch, N, [(_fused[0], G_run), (T, G_run)] if _fused else [(T, G_run)], pp)
+    rc = _timed_call(launch, N, [(_fused[0], G_run), (T, G_run)] if _fused else [(T, G_run)], pp, kernels=1)
     if rc != 0:
         raise RuntimeError(f"tcq_viterbi: HIP error code {rc}")
     if _mid:
