@@ -137,11 +137,27 @@ def row_scale(W_rot: torch.Tensor, cfg: dict) -> Tuple[torch.Tensor, torch.Tenso
 
 
 @torch.no_grad()
+def _format_tables(cfg: dict, device) -> Tuple[torch.Tensor, torch.Tensor, dict]:
+    """(level table, gains, the half-integer keywords) of a format (src/liqk_v2.py:885-895): a K_hi format alternates
+    its lower format's tables on even tile rows with the higher one's on odd rows, each table premultiplied by its
+    format's scale (its d then carries no factor)."""
+    if "K_hi" not in cfg:
+        return (torch.tensor(cfg["lut"], dtype=torch.float32, device=device), make_gains(cfg["h"], cfg["step"], device),
+                {})
+    lo, hi = TCQ_CONFIG[cfg["lo"]], TCQ_CONFIG[cfg["hi"]]
+    lut = torch.tensor(lo["lut"], dtype=torch.float32, device=device) * lo["scale"]
+    hi_kw = {"small_hi": torch.tensor(hi["lut"], dtype=torch.float32, device=device) * hi["scale"],
+             "gains_hi": make_gains(hi["h"], hi["step"], device), "mix": SUBBLOCK_SIZE}
+    return lut, make_gains(lo["h"], lo["step"], device), hi_kw
+
+
 def _quantize_rows_tcq_ldlq(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: torch.Tensor, diag_w: torch.Tensor,
                             spec_name: str, n_pass: int = 2,
                             fed: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Block16-LDLQ with every 16-column sub-block quantized in 16 x 16 tiles by the TCQ Viterbi
-    (src/liqk_v2.py:877-1021, the row-scale branch; n_pass belongs to the branch without row scale and is unused).
+    (src/liqk_v2.py:877-1021, the row-scale branch: tail-biting tiles, tiles whose trellis state carries over from
+    the previous sub-block of the same rows, half-integer formats; n_pass belongs to the branch without row scale
+    and is unused).
     Returns (d_full [M, K/256] fp16, W_hat_rot [M, K]). If fed [M, K] fp32 is given, it receives the value of every
     weight at the moment its sub-block was quantized (the Viterbi input times d)."""
     return _ldlq_rows(W_rot, U.unsqueeze(0), U_blks_inv.unsqueeze(0), diag_w.unsqueeze(0), spec_name, fed=fed)
@@ -159,11 +175,12 @@ def _ldlq_rows(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: torch.Tensor, d
     copy and first tiles). Every sum is a fixed-order fma chain, so the loop is a defined function of its inputs.
     With PACK, appends the group's fields to PACK["groups"]."""
     cfg = TCQ_CONFIG[spec_name]
-    if not cfg.get("row_scale") or "K_hi" in cfg or (cfg.get("carry") and not cfg.get("tb")):
-        raise NotImplementedError(f"{spec_name}: the GPU path serves the tail-biting row-scale formats")
+    if not cfg.get("row_scale"):
+        if U.shape[0] != 1 or fed is not None:
+            raise NotImplementedError(f"{spec_name}: formats without row scale quantize one matrix at a time")
+        return _ldlq_rows_dcand(W_rot, U[0], U_blks_inv[0], diag_w[0], cfg, spec_name)
     device = W_rot.device
-    lut = torch.tensor(cfg["lut"], dtype=torch.float32, device=device)
-    gains = make_gains(cfg["h"], cfg["step"], device)
+    lut, gains, hi_kw = _format_tables(cfg, device)
     M, K = W_rot.shape
     n_mat = U.shape[0]
     R = M // n_mat
@@ -192,6 +209,7 @@ def _ldlq_rows(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: torch.Tensor, d
     d_full = d_rb_all.to(torch.float16)
     lib = _lib.lib()
     stream = _lib.stream_ptr()
+    carry = None  # end states of the previous sub-block's tiles (carried-state formats), across blocks as well
     x_cur = torch.empty((nt, QK_K), dtype=torch.float32, device=device)
     x_nxt = torch.empty_like(x_cur)
     w_sub = W_work[:, :QK_K].clone()      # the working copy of the block being quantized
@@ -212,11 +230,21 @@ def _ldlq_rows(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: torch.Tensor, d
         codes = (pk["idx"][:, c0:], pk["idx"].stride(0), pk["gi"][:, c0:], pk["gi"].stride(0)) if pk else None
         for ib in range(NUM_SUBBLOCKS):
             s1 = (ib + 1) * SUBBLOCK_SIZE
-            out = viterbi_ub_cuda(x_cur, lut, cfg["K"], cfg["nu"], cfg["m"], gains, sub=sub, wts=wts_blk[ib],
-                                  n_cand=n_cand, tail_biting=True, tb_window=tb_window,
-                                  m_extra=cfg.get("m_extra", ()), pair_parity=cfg.get("pp", False),
-                                  return_code=pk is not None, _raw_code=True)
-            rec, code = out if pk is not None else (out, None)
+            if cfg.get("tb"):
+                out = viterbi_ub_cuda(x_cur, lut, cfg["K"], cfg["nu"], cfg["m"], gains, sub=sub, wts=wts_blk[ib],
+                                      n_cand=n_cand, tail_biting=True, tb_window=tb_window,
+                                      m_extra=cfg.get("m_extra", ()), pair_parity=cfg.get("pp", False),
+                                      return_code=pk is not None, _raw_code=True)
+                rec, code = out if pk is not None else (out, None)
+            elif cfg.get("carry"):  # the trellis state carries over to the next sub-block's tile of the same rows
+                rec, carry = viterbi_ub_cuda(x_cur, lut, cfg["K"], cfg["nu"], cfg["m"], gains, sub=SUBBLOCK_SIZE,
+                                             wts=wts_blk[ib], init_state=carry, return_end_state=True, n_cand=n_cand,
+                                             **hi_kw)
+                code = None
+            else:
+                rec = viterbi_ub_cuda(x_cur, lut, cfg["K"], cfg["nu"], cfg["m"], gains, sub=SUBBLOCK_SIZE,
+                                      wts=wts_blk[ib], n_cand=n_cand, **hi_kw)
+                code = None
             # G, the error feedback, the next sub-block's tiles and (PACK) the code / gain index scatter
             _check(lib.ltq_ldlq_sub(w_sub.data_ptr(), QK_K, rec.data_ptr(), d_rb.data_ptr(), nblocks,
                                     U_blk_inv.data_ptr(), QK_K, U_blk.data_ptr(), K, ib,
@@ -240,6 +268,101 @@ def _ldlq_rows(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: torch.Tensor, d
     if pk is not None:
         PACK["groups"].append({"spec": spec_name, "d_row": d_row, "e": e_rb, "idx": pk["idx"], "gi": pk["gi"],
                                "G": pk["G"]})
+    return d_full, W_hat_rot
+
+
+def _sq_sum(a: torch.Tensor) -> torch.Tensor:
+    """Per column of a [256, M] (rows of the block's E-shaped products): the float64 sum of squares."""
+    return a.double().square().sum(dim=0)
+
+
+def _ldlq_rows_dcand(W_rot: torch.Tensor, U: torch.Tensor, U_blks_inv: torch.Tensor, diag_w: torch.Tensor, cfg: dict,
+                     spec_name: str, n_pass: int = 2) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The branch without row scale (src/liqk_v2.py:982-1016). Per 256-column block: d_cand = fp16(rms of the
+    block's start row * scale); n_pass passes of the sub-block loop with d = d_cand (tiles start free, or carry
+    the state over), each followed by the least-squares refit d_refit = fp16(<A, B> / <B, B>) in the whitened
+    space (A = w_start U_inv, B = G U_inv) and a per-row choice of the lower loss |A - d B|^2 between d_cand and
+    d_refit (strictly lower replaces; the next pass starts from d_refit); the chosen d and its pass's G give the
+    block's reconstruction and error feedback. The sub-block loop and every product with U_inv are the fixed-order
+    kernels of the row-scale path; the block rms, the refit's inner products and the losses are float64 sums
+    (the reference's are device fp32 reductions of no fixed order), so the oracle matches bit for bit."""
+    device = W_rot.device
+    lut, gains, hi_kw = _format_tables(cfg, device)
+    M, K = W_rot.shape
+    assert M % 16 == 0, "TCQ: number of rows must be divisible by 16"
+    nt, nblocks = M // 16, K // QK_K
+    n_cand = int(os.environ.get("TCQ_NCAND", cfg.get("n_cand", 0)))
+    scale = torch.tensor(float(cfg.get("scale", 1.0)), dtype=torch.float32)
+    lib, stream = _lib.lib(), _lib.stream_ptr()
+    U, U_blks_inv = U.contiguous(), U_blks_inv.contiguous()
+    W_work = W_rot.float().clone()
+    W_hat_rot = torch.empty_like(W_work)
+    d_full = torch.empty((M, nblocks), dtype=torch.float16, device=device)
+    w_sub = torch.empty((M, QK_K), dtype=torch.float32, device=device)
+    x_cur = torch.empty((nt, QK_K), dtype=torch.float32, device=device)
+    x_nxt = torch.empty_like(x_cur)
+    G_pass = torch.empty((M, QK_K), dtype=torch.float32, device=device)
+    zero_g = torch.zeros((M, QK_K), dtype=torch.float32, device=device)
+    zero_d = torch.zeros(M, dtype=torch.float32, device=device)
+    minus_one = torch.full((M,), -1.0, dtype=torch.float32, device=device)
+    A_t = torch.empty((QK_K, M), dtype=torch.float32, device=device)
+    B_t = torch.empty_like(A_t)
+    E_t = torch.empty_like(A_t)
+    carry = None
+    for ibl in range(nblocks):
+        c0, c1 = ibl * QK_K, (ibl + 1) * QK_K
+        w_start = W_work[:, c0:c1]
+        U_blk, U_blk_inv = U[c0:c1, c0:c1], U_blks_inv[ibl]
+        rms = w_start.double().square().mean(dim=1).sqrt().float()
+        d_cand = (rms * scale.to(device)).to(torch.float16).float().clamp(min=1e-8)
+        wts_blk = diag_w[c0:c1].reshape(NUM_SUBBLOCKS, 1, SUBBLOCK_SIZE).expand(NUM_SUBBLOCKS, 16, SUBBLOCK_SIZE)
+        wts_blk = wts_blk.reshape(NUM_SUBBLOCKS, 16 * SUBBLOCK_SIZE)
+        # A = w_start U_inv: the error kernel with d = 0 (w - 0 G)
+        _check(lib.ltq_ldlq_err(w_start.data_ptr(), K, zero_g.data_ptr(), QK_K, zero_d.data_ptr(), 1,
+                                U_blk_inv.data_ptr(), QK_K, A_t.data_ptr(), M, None, 0, M, 0, 0, stream), "ltq_ldlq_err")
+        best_loss = torch.full((M,), float("inf"), dtype=torch.float64, device=device)
+        best_d = d_cand.clone()
+        G_best = torch.zeros((M, QK_K), dtype=torch.float32, device=device)
+        for _ in range(n_pass):
+            w_sub.copy_(w_start)
+            _check(lib.ltq_ldlq_prep(w_sub.data_ptr(), QK_K, d_cand.data_ptr(), 1, x_cur.data_ptr(), M, stream),
+                   "ltq_ldlq_prep")
+            for ib in range(NUM_SUBBLOCKS):
+                s1 = (ib + 1) * SUBBLOCK_SIZE
+                if cfg.get("carry"):
+                    rec, carry = viterbi_ub_cuda(x_cur, lut, cfg["K"], cfg["nu"], cfg["m"], gains, sub=SUBBLOCK_SIZE,
+                                                 wts=wts_blk[ib], init_state=carry, return_end_state=True,
+                                                 n_cand=n_cand, **hi_kw)
+                else:
+                    rec = viterbi_ub_cuda(x_cur, lut, cfg["K"], cfg["nu"], cfg["m"], gains, sub=SUBBLOCK_SIZE,
+                                          wts=wts_blk[ib], n_cand=n_cand, **hi_kw)
+                _check(lib.ltq_ldlq_sub(w_sub.data_ptr(), QK_K, rec.data_ptr(), d_cand.data_ptr(), 1,
+                                        U_blk_inv.data_ptr(), QK_K, U_blk.data_ptr(), K, ib, G_pass.data_ptr(), QK_K,
+                                        x_nxt.data_ptr() if s1 < QK_K else None, M, None, None, 0, None, 0, None, 0,
+                                        0, 0, 0, stream), "ltq_ldlq_sub")
+                x_cur, x_nxt = x_nxt, x_cur
+            # B = G U_inv: the error kernel with w = 0, d = -1 (0 - (-1) G = G exactly)
+            _check(lib.ltq_ldlq_err(zero_g.data_ptr(), QK_K, G_pass.data_ptr(), QK_K, minus_one.data_ptr(), 1,
+                                    U_blk_inv.data_ptr(), QK_K, B_t.data_ptr(), M, None, 0, M, 0, 0, stream),
+                   "ltq_ldlq_err")
+            Ad, Bd = A_t.double(), B_t.double()
+            num, den = (Ad * Bd).sum(dim=0), _sq_sum(B_t).clamp(min=1e-12)
+            d_refit = torch.where(den > 0, num / den, d_cand.double()).float().to(torch.float16).float().clamp(min=1e-8)
+            for d_try in (d_cand, d_refit):
+                loss = (Ad - d_try.double().unsqueeze(0) * Bd).square().sum(dim=0)
+                imp = loss < best_loss
+                best_loss = torch.where(imp, loss, best_loss)
+                best_d = torch.where(imp, d_try, best_d)
+                G_best = torch.where(imp.unsqueeze(1), G_pass, G_best)
+            d_cand = d_refit
+        # the block's reconstruction fl(d G) and error (w_start - d G) U_inv with the chosen scale and pass
+        _check(lib.ltq_ldlq_err(w_start.data_ptr(), K, G_best.data_ptr(), QK_K, best_d.data_ptr(), 1,
+                                U_blk_inv.data_ptr(), QK_K, E_t.data_ptr(), M, W_hat_rot[:, c0:].data_ptr(), K, M, 0,
+                                0, stream), "ltq_ldlq_err")
+        d_full[:, ibl] = best_d.to(torch.float16)
+        if c1 < K:
+            _check(lib.ltq_ldlq_update(W_work[:, c1:].data_ptr(), K, E_t.data_ptr(), M, U[c0:c1, c1:].data_ptr(), K,
+                                       M, K - c1, None, 0, None, None, 0, 0, 0, stream), "ltq_ldlq_update")
     return d_full, W_hat_rot
 
 

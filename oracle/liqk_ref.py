@@ -146,15 +146,23 @@ def _ptr(a):
 
 
 def quantize_rows_ref(W_rot, U, U_blks_inv, diag_w, cfg: dict, gains: np.ndarray, tb_window: int = 32,
-                      n_cand: int | None = None, d_rb_all=None, mistake: str = "", trace: dict | None = None):
+                      n_cand: int | None = None, d_rb_all=None, mistake: str = "", trace: dict | None = None,
+                      lut=None, hi: dict | None = None):
     """The row quantizer's LDLQ loop (src/liqk_v2.py:948-980, row-scale branch) over the C oracle's Viterbi and
     its LDLQ restatements (oracle/ldlq_oracle.c: fma chains in ascending order, as the kernels define the sums).
-    Returns (d_full fp16 [M, nblk], W_hat_rot [M, K], codes {idx int16, gi uint8}, fed [M, K]): fed holds every
-    weight's value when its sub-block was quantized. d_rb_all may be given ([M, nblk]); by default the row scale
+    Tiles are tail-biting (cfg "tb"), or carry the trellis state from one sub-block to the next (cfg "carry",
+    src/liqk_v2.py:926-929), or start free. lut overrides cfg["lut"]; hi = {"small_hi", "gains_hi"} gives a
+    half-integer format's odd-row tables (src/liqk_v2.py:887-892: the caller premultiplies each table by its
+    format's scale). Returns (d_full fp16 [M, nblk], W_hat_rot [M, K], codes {idx int16, gi uint8} (tail-biting
+    formats, else None), fed [M, K]): fed holds every weight's value when its sub-block was quantized. d_rb_all may be given ([M, nblk]); by default the row scale
     comes from row_scale_ref. `mistake` plants one error for the tests that check the identities catch it:
     "sign" (the sub-block feedback added instead of subtracted), "slice" (the inter-block update from the
     factor's rows shifted by one) or "index" (the next sub-block fed from the wrong column). With a `trace`
     dict, trace["x"] [M, K] receives the Viterbi inputs in matrix layout."""
+    if not cfg.get("row_scale"):
+        d_full, W_hat = quantize_rows_dcand_ref(W_rot, U, U_blks_inv, diag_w, cfg, gains, n_cand=n_cand, lut=lut,
+                                                hi=hi)
+        return d_full, W_hat, None, None
     L = ref.lib()
     W = np.ascontiguousarray(W_rot.numpy() if hasattr(W_rot, "numpy") else W_rot, np.float32)
     Uf = np.ascontiguousarray(U.numpy() if hasattr(U, "numpy") else U, np.float32)
@@ -163,7 +171,10 @@ def quantize_rows_ref(W_rot, U, U_blks_inv, diag_w, cfg: dict, gains: np.ndarray
     M, K = W.shape
     nt, nblocks = M // 16, K // QK_K
     n_cand = cfg.get("n_cand", 0) if n_cand is None else n_cand
-    lut = np.asarray(cfg["lut"], np.float32)
+    lut = np.asarray(cfg["lut"] if lut is None else lut, np.float32)
+    hi_kw = {} if hi is None else dict(small_hi=np.asarray(hi["small_hi"], np.float32),
+                                       gains_hi=np.asarray(hi["gains_hi"], np.float32), mix=SUB)
+    carry = None
     m_extra = tuple(cfg.get("m_extra", ()))
     if d_rb_all is None:
         _, _, _, d_rb_all = row_scale_ref(W, cfg)
@@ -193,13 +204,21 @@ def quantize_rows_ref(W_rot, U, U_blks_inv, diag_w, cfg: dict, gains: np.ndarray
             wts = np.tile(dw[c0 + s0:c0 + s1], 16)
             if xs_all is not None:
                 xs_all[:, c0 + s0:c0 + s1] = x.reshape(M, SUB)
-            rec, gi, ix = ref.viterbi_ub_cuda_ref(x, lut, cfg["K"], 10, cfg["m"], gains, sub=cfg.get("sub", 16),
-                                                  wts=wts, n_cand=n_cand, tail_biting=True, tb_window=tb_window,
-                                                  m_extra=m_extra, pair_parity=int(cfg.get("pp", 0)),
-                                                  return_code=True)
+            if cfg.get("tb"):
+                rec, gi, ix = ref.viterbi_ub_cuda_ref(x, lut, cfg["K"], 10, cfg["m"], gains, sub=cfg.get("sub", 16),
+                                                      wts=wts, n_cand=n_cand, tail_biting=True, tb_window=tb_window,
+                                                      m_extra=m_extra, pair_parity=int(cfg.get("pp", 0)),
+                                                      return_code=True)
+                idx[:, c0 + s0:c0 + s1] = np.asarray(ix).reshape(M, SUB).astype(np.int16)
+                gim[:, c0 + s0:c0 + s1] = np.asarray(gi).reshape(M, SUB).astype(np.uint8)
+            elif cfg.get("carry"):  # the state carries over to the next sub-block (src/liqk_v2.py:926-929)
+                rec, carry = ref.viterbi_ub_cuda_ref(x, lut, cfg["K"], 10, cfg["m"], gains, sub=SUB, wts=wts,
+                                                     init_state=carry, return_end_state=True, n_cand=n_cand, **hi_kw)
+                carry = np.ascontiguousarray(carry, np.int32)
+            else:
+                rec = ref.viterbi_ub_cuda_ref(x, lut, cfg["K"], 10, cfg["m"], gains, sub=SUB, wts=wts, n_cand=n_cand,
+                                              **hi_kw)
             rec = np.ascontiguousarray(rec, np.float32)
-            idx[:, c0 + s0:c0 + s1] = np.asarray(ix).reshape(M, SUB).astype(np.int16)
-            gim[:, c0 + s0:c0 + s1] = np.asarray(gi).reshape(M, SUB).astype(np.uint8)
             x_next = np.empty((nt, 256), np.float32)
             L.ltq_oracle_ldlq_sub(_ptr(w_sub), QK_K, _ptr(rec), _ptr(d), 1, _ptr(Ubi_b), QK_K, _ptr(U_blk), QK_K, ib,
                                   _ptr(G), QK_K, _ptr(x_next) if s1 < QK_K else None, M, _ptr(fed_b), QK_K)
@@ -222,7 +241,105 @@ def quantize_rows_ref(W_rot, U, U_blks_inv, diag_w, cfg: dict, gains: np.ndarray
     d_full = d_all.astype(np.float16)
     if trace is not None:
         trace["x"] = xs_all
-    return d_full, W_hat, {"idx": idx, "gi": gim}, fed
+    return d_full, W_hat, ({"idx": idx, "gi": gim} if cfg.get("tb") else None), fed
+
+
+def quantize_rows_dcand_ref(W_rot, U, U_blks_inv, diag_w, cfg: dict, gains: np.ndarray, n_pass: int = 2,
+                            n_cand: int | None = None, lut=None, hi: dict | None = None, mistake: str = "",
+                            trace: dict | None = None):
+    """The branch without row scale (src/liqk_v2.py:982-1016): per 256-column block, d_cand = fp16(rms * scale)
+    of the block's start rows, n_pass passes of the sub-block loop at d_cand (tiles start free, or carry the
+    state over with cfg "carry"), each followed by the refit d_refit = fp16(<A, B> / <B, B>) with A = w_start
+    U_inv and B = G U_inv, and the per-row choice of the strictly lower |A - d B|^2 between d_cand and d_refit;
+    the next pass starts from d_refit. The products with U_inv and the feedback are the oracle's fma chains; the
+    rms, the inner products and the losses are float64 sums. Returns (d_full fp16 [M, nblk], W_hat [M, K]).
+    `mistake` "no_refit" keeps d_cand in every pass (for the test that the refit is pinned). With a `trace` dict,
+    trace["blocks"][b] lists every pass's (d_cand, G, d_refit) and trace["start"][b] the block's start rows."""
+    L = ref.lib()
+    W = np.ascontiguousarray(W_rot.numpy() if hasattr(W_rot, "numpy") else W_rot, np.float32)
+    Uf = np.ascontiguousarray(U.numpy() if hasattr(U, "numpy") else U, np.float32)
+    Ubi = np.ascontiguousarray(U_blks_inv.numpy() if hasattr(U_blks_inv, "numpy") else U_blks_inv, np.float32)
+    dw = np.ascontiguousarray(diag_w.numpy() if hasattr(diag_w, "numpy") else diag_w, np.float32)
+    M, K = W.shape
+    nt, nblocks = M // 16, K // QK_K
+    n_cand = cfg.get("n_cand", 0) if n_cand is None else n_cand
+    lut = np.asarray(cfg["lut"] if lut is None else lut, np.float32)
+    hi_kw = {} if hi is None else dict(small_hi=np.asarray(hi["small_hi"], np.float32),
+                                       gains_hi=np.asarray(hi["gains_hi"], np.float32), mix=SUB)
+    scale = np.float32(cfg.get("scale", 1.0))
+    W_work = W.copy()
+    W_hat = np.empty_like(W)
+    d_full = np.empty((M, nblocks), np.float16)
+    zero_g = np.zeros((M, QK_K), np.float32)
+    carry = None
+    for ibl in range(nblocks):
+        c0, c1 = ibl * QK_K, (ibl + 1) * QK_K
+        w_start = np.ascontiguousarray(W_work[:, c0:c1])
+        U_blk = np.ascontiguousarray(Uf[c0:c1, c0:c1])
+        Ubi_b = Ubi[ibl]
+        rms = np.sqrt(np.mean(np.square(w_start.astype(np.float64)), axis=1)).astype(np.float32)
+        d_cand = np.maximum((rms * scale).astype(np.float16).astype(np.float32), np.float32(1e-8))
+        A = np.empty((M, QK_K), np.float32)
+        L.ltq_oracle_ldlq_err(_ptr(w_start), QK_K, _ptr(zero_g), QK_K, _ptr(np.zeros(M, np.float32)), 1,
+                              _ptr(Ubi_b), QK_K, _ptr(A), QK_K, None, QK_K, M)
+        best_loss = np.full(M, np.inf)
+        best_d = d_cand.copy()
+        G_best = np.zeros((M, QK_K), np.float32)
+        passes = []
+        if trace is not None:
+            trace.setdefault("blocks", []).append(passes)
+            trace.setdefault("start", []).append(w_start.copy())
+        for _ in range(n_pass):
+            w_sub = w_start.copy()
+            G = np.empty((M, QK_K), np.float32)
+            x = np.ascontiguousarray((w_sub[:, :SUB] * (np.float32(1) / d_cand)[:, None]).reshape(nt, 256))
+            for ib in range(QK_K // SUB):
+                s0, s1 = ib * SUB, (ib + 1) * SUB
+                wts = np.tile(dw[c0 + s0:c0 + s1], 16)
+                if cfg.get("carry"):
+                    rec, carry = ref.viterbi_ub_cuda_ref(x, lut, cfg["K"], 10, cfg["m"], gains, sub=SUB, wts=wts,
+                                                         init_state=carry, return_end_state=True, n_cand=n_cand,
+                                                         **hi_kw)
+                    carry = np.ascontiguousarray(carry, np.int32)
+                else:
+                    rec = ref.viterbi_ub_cuda_ref(x, lut, cfg["K"], 10, cfg["m"], gains, sub=SUB, wts=wts,
+                                                  n_cand=n_cand, **hi_kw)
+                rec = np.ascontiguousarray(rec, np.float32)
+                x_next = np.empty((nt, 256), np.float32)
+                L.ltq_oracle_ldlq_sub(_ptr(w_sub), QK_K, _ptr(rec), _ptr(d_cand), 1, _ptr(Ubi_b), QK_K, _ptr(U_blk),
+                                      QK_K, ib, _ptr(G), QK_K, _ptr(x_next) if s1 < QK_K else None, M, None, QK_K)
+                x = x_next
+            B = np.empty((M, QK_K), np.float32)
+            L.ltq_oracle_ldlq_err(_ptr(zero_g), QK_K, _ptr(G), QK_K, _ptr(np.full(M, -1.0, np.float32)), 1,
+                                  _ptr(Ubi_b), QK_K, _ptr(B), QK_K, None, QK_K, M)
+            Ad, Bd = A.astype(np.float64), B.astype(np.float64)
+            num, den = np.sum(Ad * Bd, axis=1), np.maximum(np.sum(Bd * Bd, axis=1), 1e-12)
+            ratio = np.where(den > 0, num / den, d_cand.astype(np.float64)).astype(np.float32)
+            d_refit = np.maximum(ratio.astype(np.float16).astype(np.float32), np.float32(1e-8))
+            if mistake == "no_refit":
+                d_refit = d_cand
+            passes.append((d_cand.copy(), G.copy(), d_refit.copy()))
+            for d_try in (d_cand, d_refit):
+                loss = np.sum(np.square(Ad - d_try.astype(np.float64)[:, None] * Bd), axis=1)
+                imp = loss < best_loss
+                best_loss = np.where(imp, loss, best_loss)
+                best_d = np.where(imp, d_try, best_d)
+                G_best = np.where(imp[:, None], G, G_best)
+            d_cand = d_refit
+        E = np.empty((M, QK_K), np.float32)
+        wh = np.empty((M, QK_K), np.float32)
+        G_best = np.ascontiguousarray(G_best, np.float32)
+        best_d = np.ascontiguousarray(best_d, np.float32)
+        L.ltq_oracle_ldlq_err(_ptr(w_start), QK_K, _ptr(G_best), QK_K, _ptr(best_d), 1, _ptr(Ubi_b), QK_K, _ptr(E),
+                              QK_K, _ptr(wh), QK_K, M)
+        W_hat[:, c0:c1] = wh
+        d_full[:, ibl] = best_d.astype(np.float16)
+        if c1 < K:
+            Up = np.ascontiguousarray(Uf[c0:c1, c1:])
+            rest = np.ascontiguousarray(W_work[:, c1:])
+            L.ltq_oracle_ldlq_update(_ptr(rest), K - c1, _ptr(E), QK_K, _ptr(Up), K - c1, M, K - c1)
+            W_work[:, c1:] = rest
+    return d_full, W_hat
 
 
 def ldlq_identity_residual(W_rot, W_hat, fed, U, U_blks_inv):

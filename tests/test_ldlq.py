@@ -126,6 +126,103 @@ def test_oracle_ldlq_without_feedback_is_plain_quantization():
             assert np.array_equal(Wh[:, c:c + 16], d[:, None] * np.asarray(rec, np.float32).reshape(32, 16))
 
 
+def test_oracle_carried_state_threads_through_sub_blocks():
+    """H = I (no feedback): a carried-state format (TCQ3R) quantizes the sub-blocks of each row group in order,
+    every tile starting from the end state of the same rows' previous tile, across 256-column blocks too
+    (src/liqk_v2.py:926-929); starting every tile free gives a different reconstruction."""
+    from oracle import liqk_ref, ref
+    from ltq_amd.formats import TCQ_CONFIG
+    cfg = TCQ_CONFIG["TCQ3R"]
+    W, H = _synthetic(32, 512, seed=4)
+    U, dw, Ubi = liqk_ref.factor_hessian_ref(torch.eye(512), 0.2)
+    gains, _, _ = _oracle_tables(cfg)
+    d_full, Wh, codes, fed = liqk_ref.quantize_rows_ref(W, U, Ubi, dw, cfg, gains)
+    assert codes is None
+    Wn, lut = W.numpy(), np.asarray(cfg["lut"], np.float32)
+    _, _, _, d_all = liqk_ref.row_scale_ref(W, cfg)
+    carry = None
+    free = np.empty_like(Wn)
+    for b in range(2):
+        d = np.maximum(d_all[:, b], np.float32(1e-8))
+        for j in range(16):
+            c = 256 * b + 16 * j
+            x = (Wn[:, c:c + 16] * (np.float32(1) / d)[:, None]).reshape(2, 256)
+            wts = np.tile(dw[c:c + 16].numpy(), 16)
+            rec, carry = ref.viterbi_ub_cuda_ref(x, lut, 3, 10, 359, gains, wts=wts, init_state=carry,
+                                                 return_end_state=True)
+            assert np.array_equal(Wh[:, c:c + 16], d[:, None] * np.asarray(rec, np.float32).reshape(32, 16))
+            rec0 = ref.viterbi_ub_cuda_ref(x, lut, 3, 10, 359, gains, wts=wts)
+            free[:, c:c + 16] = d[:, None] * np.asarray(rec0, np.float32).reshape(32, 16)
+    assert not np.array_equal(free, Wh)
+
+
+def test_oracle_half_integer_rows_use_their_tables():
+    """TCQ25R (H = I): even rows of every 16-row group take TCQ2R's tables, odd rows TCQ3R's, each premultiplied
+    by its format's scale (src/liqk_v2.py:887-892): every reconstructed value / d is a product gain x level of
+    its row's tables, and the odd rows use levels only the higher table has."""
+    from oracle import liqk_ref
+    from ltq_amd.formats import TCQ_CONFIG
+    cfg = TCQ_CONFIG["TCQ25R"]
+    W, _ = _synthetic(32, 512, seed=5)
+    U, dw, Ubi = liqk_ref.factor_hessian_ref(torch.eye(512), 0.2)
+    gains, lut, hi = _oracle_tables(cfg)
+    _, Wh, _, _ = liqk_ref.quantize_rows_ref(W, U, Ubi, dw, cfg, gains, lut=lut, hi=hi)
+    _, _, _, d_all = liqk_ref.row_scale_ref(W, cfg)
+    lo_vals = np.unique(np.float32(gains)[:, None] * np.float32(lut)[None, :])
+    hi_vals = np.unique(np.float32(hi["gains_hi"])[:, None] * np.float32(hi["small_hi"])[None, :])
+    d = np.maximum(d_all, np.float32(1e-8))
+    only_hi = 0
+    for i in range(32):
+        vals = hi_vals if i % 2 else lo_vals
+        for b in range(2):
+            allowed = set((d[i, b] * vals).tolist())  # W_hat = fl(d fl(gain level))
+            row = Wh[i, 256 * b:256 * (b + 1)]
+            assert all(float(v) in allowed for v in row), (i, b)
+            if i % 2:
+                only_hi += sum(float(v) not in set((d[i, b] * lo_vals).tolist()) for v in row)
+    assert only_hi > 0
+
+
+def test_oracle_dcand_branch_pins():
+    """The branch without row scale (TCQ3, src/liqk_v2.py:982-1016) with H = I (U = c I, so the whitened
+    products are the raw ones over c): the first d_cand is fp16 of the block's rms times the format's scale,
+    each pass's d_refit is fp16 of the least-squares ratio <w, G> / <G, G> of that pass, the next pass starts from
+    it, and every row keeps the (scale, pass) of least |w - d G|^2, the earlier on ties; the reconstruction is
+    fl(d G) of that choice. Keeping d_cand (no refit) changes the result."""
+    from oracle import liqk_ref
+    from ltq_amd.formats import TCQ_CONFIG
+    cfg = TCQ_CONFIG["TCQ3"]
+    W, _ = _synthetic(32, 512, seed=6)
+    U, dw, Ubi = liqk_ref.factor_hessian_ref(torch.eye(512), 0.2)
+    gains, _, _ = _oracle_tables(cfg)
+    tr = {}
+    d_full, Wh = liqk_ref.quantize_rows_dcand_ref(W, U, Ubi, dw, cfg, gains, trace=tr)
+    Wn = W.numpy()
+    f16 = lambda a: np.maximum(np.asarray(a, np.float32).astype(np.float16).astype(np.float32), np.float32(1e-8))
+    for b, passes in enumerate(tr["blocks"]):
+        w = Wn[:, 256 * b:256 * (b + 1)].astype(np.float64)
+        assert np.array_equal(tr["start"][b], Wn[:, 256 * b:256 * (b + 1)])  # H = I: no feedback between blocks
+        rms = np.sqrt(np.mean(w * w, axis=1)).astype(np.float32)
+        assert np.array_equal(passes[0][0], f16(rms * np.float32(cfg["scale"])))
+        tries = []
+        for p, (d_c, G, d_r) in enumerate(passes):
+            g = G.astype(np.float64)
+            ls = f16(np.sum(w * g, axis=1) / np.sum(g * g, axis=1))
+            assert np.mean(ls == d_r) >= 0.99 and np.all(np.abs(ls - d_r) <= np.abs(d_r) * 2.0 ** -10)
+            if p > 0:
+                assert np.array_equal(d_c, passes[p - 1][2])
+            tries += [(d_c, G), (d_r, G)]
+        loss = np.stack([np.sum((w - d.astype(np.float64)[:, None] * G.astype(np.float64)) ** 2, axis=1)
+                         for d, G in tries])
+        pick = np.argmin(loss, axis=0)  # first minimum
+        for i in range(32):
+            d, G = tries[pick[i]]
+            assert np.array_equal(Wh[i, 256 * b:256 * (b + 1)], d[i] * G[i]), (b, i)
+            assert d_full[i, b] == np.float16(d[i])
+    _, Wh_nr = liqk_ref.quantize_rows_dcand_ref(W, U, Ubi, dw, cfg, gains, mistake="no_refit")
+    assert not np.array_equal(Wh_nr, Wh)
+
+
 # ---------------------------------------------------------------------------------------------- GPU
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N", [(64, 256), (256, 1024), (4096, 512)])
@@ -212,7 +309,23 @@ def test_gpu_ldlq_sub_bit_exact(oracle):
 
 
 ROW_CASES = [("TCQ275X2", 64, 768, False), ("TCQ275X", 64, 768, False), ("TCQ25X", 64, 768, False),
-             ("TCQ375X", 64, 768, False), ("TCQ3X3", 64, 768, True), ("TCQ275X2", 256, 2048, False)]
+             ("TCQ375X", 64, 768, False), ("TCQ3X3", 64, 768, True), ("TCQ275X2", 256, 2048, False),
+             ("TCQ3R", 64, 768, False), ("TCQ4RH3", 64, 768, False), ("TCQ25R", 64, 768, False),
+             ("TCQ35R", 48, 512, False), ("TCQ3", 64, 768, False), ("TCQ4", 48, 512, False)]
+
+
+def _oracle_tables(cfg):
+    """(gains, lut, hi) for quantize_rows_ref: a half-integer format's tables premultiplied by their formats'
+    scales (src/liqk_v2.py:887-892), gains evaluated on the CPU as the quantizer's are."""
+    from ltq_amd.formats import TCQ_CONFIG
+    from ltq_amd.tcq_proto import make_gains
+    if "K_hi" not in cfg:
+        return make_gains(cfg["h"], cfg["step"], "cpu").numpy(), None, None
+    lo, hi = TCQ_CONFIG[cfg["lo"]], TCQ_CONFIG[cfg["hi"]]
+    lut = np.asarray(lo["lut"], np.float32) * np.float32(lo["scale"])
+    return (make_gains(lo["h"], lo["step"], "cpu").numpy(), lut,
+            {"small_hi": np.asarray(hi["lut"], np.float32) * np.float32(hi["scale"]),
+             "gains_hi": make_gains(hi["h"], hi["step"], "cpu").numpy()})
 
 
 @pytest.mark.gpu
@@ -220,38 +333,41 @@ ROW_CASES = [("TCQ275X2", 64, 768, False), ("TCQ275X", 64, 768, False), ("TCQ25X
 def test_gpu_quantize_rows_bit_exact(spec, M, K, identity_h):
     """The GPU row quantizer against the oracle on the same rotated rows and factors: codes, gain indices, tile
     values, reconstruction, fed values and block scales bit for bit (C3 formats with a real Hessian and outlier
-    columns; C2's TCQ3X3 with gain candidates and H = I)."""
+    columns; C2's TCQ3X3 with gain candidates and H = I; carried-state formats, with gain candidates and
+    half-integer tables)."""
     from oracle import liqk_ref
     from ltq_amd import liqk, rotation
-    from ltq_amd.formats import TCQ_CONFIG, make_format
+    from ltq_amd.formats import TCQ_CONFIG
     cfg = TCQ_CONFIG[spec]
+    tb = bool(cfg.get("tb"))
     W, H = _synthetic(M, K, outliers=max(1, K // 100))
     if identity_h:
         H = torch.eye(K)
     W_rot, H_rot, _ = rotation.compute_optimal_suh(W.to(DEV), H.to(DEV), seed=1337)
     U, diag_w, Ub_inv = liqk.factor_hessian(H_rot, 0.2)
-    fed = torch.empty((M, K), device=DEV)
+    fed = torch.empty((M, K), device=DEV) if cfg.get("row_scale") else None  # the d_cand branch has no single fed
     print(f"quantize rows {M} x {K} {spec}", flush=True)
-    liqk.PACK = {"groups": []}
+    liqk.PACK = {"groups": []} if tb else None  # .ltq fields exist for the tail-biting formats
     try:
         d_full, W_hat = liqk._quantize_rows_tcq_ldlq(W_rot, U, Ub_inv, diag_w, spec, fed=fed)
-        grp = liqk.PACK["groups"].pop()
+        grp = liqk.PACK["groups"].pop() if tb else None
     finally:
         liqk.PACK = None
     torch.cuda.synchronize()
-    f = make_format(spec)
+    gains, lut, hi = _oracle_tables(cfg)
     d_ref, Wh_ref, codes, fed_ref = liqk_ref.quantize_rows_ref(W_rot.cpu(), U.cpu(), Ub_inv.cpu(), diag_w.cpu(), cfg,
-                                                               f.gain_tab)
+                                                               gains, lut=lut, hi=hi)
     u32 = lambda a: np.ascontiguousarray(a).view(np.uint32)
-    n_idx = int((grp["idx"].cpu().numpy() != codes["idx"]).sum())
-    n_gi = int((grp["gi"].cpu().numpy() != codes["gi"]).sum())
+    n_idx = int((grp["idx"].cpu().numpy() != codes["idx"]).sum()) if tb else 0
+    n_gi = int((grp["gi"].cpu().numpy() != codes["gi"]).sum()) if tb else 0
     Wr = W_rot.cpu().numpy().astype(np.float64)
     mse_gpu = float(np.mean((Wr - W_hat.cpu().numpy()) ** 2))
     mse_ref = float(np.mean((Wr - Wh_ref) ** 2))
     print(f"{spec} {M}x{K}: code mismatches {n_idx}, gain index mismatches {n_gi}, MSE gpu {mse_gpu:.6e} "
           f"oracle {mse_ref:.6e} (relative difference {abs(mse_gpu - mse_ref) / mse_ref:.1e})", flush=True)
     assert n_idx == 0 and n_gi == 0
-    assert np.array_equal(u32(fed.cpu().numpy()), u32(fed_ref))
+    if fed is not None:
+        assert np.array_equal(u32(fed.cpu().numpy()), u32(fed_ref))
     assert np.array_equal(u32(W_hat.cpu().numpy()), u32(Wh_ref))
     assert np.array_equal(d_full.cpu().numpy().view(np.uint16), d_ref.view(np.uint16))
     assert abs(mse_gpu - mse_ref) <= 1e-6 * mse_ref

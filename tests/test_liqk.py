@@ -224,3 +224,23 @@ def test_gpu_quantize_matrix_pack_decodes_to_fields():
     b = pack_slice(pm["idx"], pm["gi"], f)
     dec = pack.decode_slice(b, M, K, f.K, f.frac, f.h, f.sub, f.masks, f.lut, f.gain_tab)
     assert np.array_equal(dec.view(np.uint32), pm["G"].cpu().numpy().view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("spec", ["TCQ3R", "TCQ25R", "TCQ3", ((0, 32, "TCQ3R"), (32, 64, "TCQ275X2"))])
+def test_gpu_quantize_matrix_other_branches(spec):
+    """The matrix driver over the carried-state, half-integer and d_cand (no row scale) branches, and a matrix
+    whose row slices mix a carried-state and a tail-biting format: the reconstruction is finite, the proxy loss
+    is the one its definition gives for the returned W_hat, and it is below that of the all-zero reconstruction."""
+    from ltq_amd import liqk
+    M, K = 64, 512
+    W, H = _synthetic(M, K, seed=2)
+    Wd, Hd = W.to(DEV), H.to(DEV)
+    print(f"quantize matrix {spec}", flush=True)
+    q, W_hat, rel = liqk.quantize_matrix_liqk_v2(Wd, Hd, spec)
+    torch.cuda.synchronize()
+    assert torch.isfinite(W_hat).all() and q["d"].shape == (M, K // 256)
+    dW = (Wd - W_hat).double()
+    expect = float(torch.trace(dW @ Hd.double() @ dW.T) / torch.trace(Wd.double() @ Hd.double() @ Wd.double().T))
+    print(f"{spec}: relative proxy loss {rel:.4f} (recomputed {expect:.4f})", flush=True)
+    assert abs(rel - expect) <= 1e-3 * expect and rel < 0.5
