@@ -12,8 +12,8 @@ over the 256 tiles of 16 rows x 16 columns (src/liqk_v2.py:917-919 -> src/tcq_pr
 feedback, then the c_row / suh refit.
 
 Prints one JSON line (driver contract). `roofline` is the dominant kernel (the Viterbi) against the gfx950
-fp32 VALU peak, from HIP events recorded around every Viterbi pass of one sub-block in 16 inside the timed
-region, on the stream the kernels run on; `cpu_baseline` is the reference's CPU path -- torch, eager, every core
+fp32 VALU peak, from HIP events carried by both Viterbi launches of one sub-block in 17 inside the timed
+region (17 is prime to the 16 sub-blocks of a column block, so every sub-block position is sampled alike); `cpu_baseline` is the reference's CPU path -- torch, eager, every core
 of this host (oracle/torch_viterbi.py restates viterbi_ub with the production semantics, pinned to the
 reference's outputs) plus the LDLQ feedback -- on the first sub-blocks of the same matrix, extrapolated to the
 whole matrix; `cpu_baseline_c_port` is the C oracle on the same tiles (Viterbi stage only).
@@ -628,12 +628,13 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    # stage marks every step; Viterbi launch events on one sub-block in 16 (both passes), so the event records
-    # do not perturb the launch stream; events around the rotation, row-scale, pack and LDLQ-update calls
+    # stage marks every step; Viterbi launch events on one sub-block in 17 (both passes; 17 is prime to the 16
+    # sub-blocks of a column block, whose first one follows the inter-block update and runs ~0.6 us slower, so
+    # every position is sampled alike); events carried by the rotation, row-scale, pack and LDLQ-update launches
     timer.active = True
     liqk.STAGE_EVENTS, tcq_proto.LAUNCH_EVENTS = [], []
     tcq_proto.EVENT_FACTORY = DeviceEvent
-    tcq_proto.LAUNCH_SAMPLE, tcq_proto._launch_count = 16, 0
+    tcq_proto.LAUNCH_SAMPLE, tcq_proto._launch_count = 17, 0
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -659,8 +660,8 @@ def main():
         if name == "start":
             continue
         stages[name] = stages.get(name, 0.0) + stage_ev[i - 1][1].elapsed_time(ev) / args.steps
-    # one record per sampled sub-block: both passes (2 * tb_window and 256 steps over rows / 16 tiles) between
-    # one event pair
+    # one record per sampled sub-block: both passes (2 * tb_window and 256 steps over rows / 16 tiles), an event
+    # pair on each launch
     secs, ops_timed, n_timed = viterbi_event_totals(launch_ev)
     avg = secs / n_timed
     n_launch = 2 * (cols // 256) * 16
@@ -683,7 +684,7 @@ def main():
                                f".ltq slice packing",
                    "format": FORMAT, "rows": rows, "cols": cols, "parallelism": "single GPU"},
         "roofline": {"bound": "valu", "timed_on": "a HIP start / stop event pair carried by each of the two Viterbi launches of "
-                                  "one sub-block in 16 (hipExtLaunchKernelGGL)", "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
+                                  "one sub-block in 17 (hipExtLaunchKernelGGL)", "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
                      "unit": "TFLOP/s (fp32 VALU lane-ops/s x 1e-12)", "frac": round(achieved / VALU_PEAK_TOPS, 4),
                      "traffic": traffic, "kernel": "tcq_viterbi_kernel<10,2,2,8,1>",
                      "avg_launch_us": round(avg * 1e6, 2), "lane_ops_per_launch": ops},
