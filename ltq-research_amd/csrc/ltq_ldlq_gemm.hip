@@ -86,9 +86,14 @@ __global__ __launch_bounds__(256, 3) void ldlq_gemm_kernel(GemmArgs p)
     if (p.rows_per_mat > 0) p.b += (row0 / p.rows_per_mat) * p.b_ms;  // a tile never straddles two matrices
     const bool write_what = EPI == 0 && p.what != nullptr && tn == 0;
 
-    // staging registers of one stage: 2 float4 of A and 2 of B per thread
-    v4f ra[2], rb[2];
+    // staging registers of one stage: 2 float4 of A and 2 of B per thread. AMODE 1 keeps its raw operands
+    // (ws, g, d) until store_stage, after the stage's MFMAs: no arithmetic or store sits between the loads and the
+    // MFMAs, so the next stage's loads fly while they run.
+    v4f ra[2], rb[2], rw[2], rg[2];
+    float rd[2];
+    int k_st = 0;  // k0 of the staged stage
     auto load_stage = [&](int k0) {
+        k_st = k0;
 #pragma unroll
         for (int q = 0; q < 2; q++) {
             const int e = tid + 256 * q;
@@ -100,19 +105,13 @@ __global__ __launch_bounds__(256, 3) void ldlq_gemm_kernel(GemmArgs p)
                 const long i = row0 + (e & 31) * 4;
                 ra[q] = i < p.M ? *(const v4f*)(p.a + (long)(k0 + kb) * p.ld_a + i) : v4f{0.f, 0.f, 0.f, 0.f};
             } else {
-                // A: output row r = e / 4, k = 4 (e % 4) .. + 3, computed as ws - d * g
+                // A: output row r = e / 4, k = 4 (e % 4) .. + 3, later ws - d * g
                 const long i = row0 + (e >> 2);
                 const int k = k0 + (e & 3) * 4;
-                if (i < p.M) {
-                    const v4f w = *(const v4f*)(p.a + i * p.ld_a + k);
-                    const v4f gg = *(const v4f*)(p.g + i * p.ldg + k);
-                    const float dd = p.d[i * p.ldd];
-                    const v4f dg = v4f{dd * gg.x, dd * gg.y, dd * gg.z, dd * gg.w};
-                    if (write_what) *(v4f*)(p.what + i * p.ld_what + k) = dg;
-                    ra[q] = w - dg;
-                } else {
-                    ra[q] = v4f{0.f, 0.f, 0.f, 0.f};
-                }
+                const bool in = i < p.M;
+                rw[q] = in ? *(const v4f*)(p.a + i * p.ld_a + k) : v4f{0.f, 0.f, 0.f, 0.f};
+                rg[q] = in ? *(const v4f*)(p.g + i * p.ldg + k) : v4f{0.f, 0.f, 0.f, 0.f};
+                rd[q] = in ? p.d[i * p.ldd] : 0.f;
             }
         }
     };
@@ -126,10 +125,15 @@ __global__ __launch_bounds__(256, 3) void ldlq_gemm_kernel(GemmArgs p)
                 *(v4f*)&sA[buf][kb][(e & 31) * 4] = ra[q];
             } else {
                 const int r = e >> 2, k = (e & 3) * 4;
-                sA[buf][k + 0][r] = ra[q].x;
-                sA[buf][k + 1][r] = ra[q].y;
-                sA[buf][k + 2][r] = ra[q].z;
-                sA[buf][k + 3][r] = ra[q].w;
+                const float dd = rd[q];
+                const v4f dg = v4f{dd * rg[q].x, dd * rg[q].y, dd * rg[q].z, dd * rg[q].w};
+                const long i = row0 + r;
+                if (write_what && i < p.M) *(v4f*)(p.what + i * p.ld_what + k_st + k) = dg;
+                const v4f a = rw[q] - dg;
+                sA[buf][k + 0][r] = a.x;
+                sA[buf][k + 1][r] = a.y;
+                sA[buf][k + 2][r] = a.z;
+                sA[buf][k + 3][r] = a.w;
             }
         }
     };
