@@ -101,6 +101,10 @@ __global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict_
     }
 }
 
+// One workgroup per 16-row tile. Every global load of the tile is issued first (its Viterbi output and codes, the
+// weights it saw and the ones it updates, the diagonal block of U_inv, the block's 16 U rows into LDS), so the
+// workgroup waits for memory about once; written as a loop over the updated columns the compiler had waited for
+// each column group's loads in turn.
 __global__ __launch_bounds__(256) void ldlq_sub_kernel(float* __restrict__ wk, long ldw, const float* __restrict__ rec,
                                                        const float* __restrict__ d, long ldd,
                                                        const float* __restrict__ uinv, long ldi,
@@ -114,25 +118,40 @@ __global__ __launch_bounds__(256) void ldlq_sub_kernel(float* __restrict__ wk, l
 {
     __shared__ float s_err[16][17];
     __shared__ float s_d[16];
+    __shared__ __align__(16) float s_u[16][256];  // U rows s0 .. s0 + 15 of the block, columns s1 .. 255
     const int tid = threadIdx.x, r = tid >> 4, c = tid & 15;
     const long row0 = (long)blockIdx.x * 16, row = row0 + r;
     if (row0 >= M) return;
-    const int s1 = s0 + 16;
+    const int s1 = s0 + 16, nj = (256 - s1) / 16;  // this thread updates columns s1 + c + 16 m, m < nj
     if (tiles_per_mat > 0) {  // stacked matrices: this tile's rows belong to matrix blockIdx.x / tiles_per_mat
         const long mat = (long)blockIdx.x / tiles_per_mat;
         uinv += mat * uinv_ms;
         ublk += mat * ublk_ms;
     }
-    if (tid < 16) s_d[tid] = d[(row0 + tid) * ldd];
     // tile element t = 16 r + c is row r, sub-block column c
     const float g = rec[(long)blockIdx.x * 256 + tid];
+    const int cv = code ? code[(long)blockIdx.x * 256 + tid] : 0;
+    const float wv = wk[row * ldw + s0 + c];  // the value this sub-block's Viterbi saw (times 1 / d)
+    float wj[15];
+#pragma unroll
+    for (int m = 0; m < 15; m++) wj[m] = m < nj ? wk[row * ldw + s1 + c + 16 * m] : 0.f;
+    float ui[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) ui[k] = uinv[(long)(s0 + k) * ldi + s0 + c];
+    {  // thread (k, group q) copies U[s0 + k][16 q .. 16 q + 15] when those columns are updated
+        const int k = tid >> 4, c0 = (tid & 15) * 16;
+        if (c0 >= s1) {
+            const float* src = ublk + (long)(s0 + k) * ldu + c0;
+#pragma unroll
+            for (int v = 0; v < 16; v++) s_u[k][c0 + v] = src[v];
+        }
+    }
+    if (tid < 16) s_d[tid] = d[(row0 + tid) * ldd];
     G[row * ldg + s0 + c] = g;
     if (code) {
-        const int cv = code[(long)blockIdx.x * 256 + tid];
         idx[row * ld_idx + s0 + c] = (int16_t)(cv & 0xFFFF);
         gi[row * ld_gi + s0 + c] = (uint8_t)(cv >> 16);
     }
-    const float wv = wk[row * ldw + s0 + c];  // the value this sub-block's Viterbi saw (times 1 / d)
     if (fed) fed[row * ld_fed + s0 + c] = wv;
     __syncthreads();
     const float dr = s_d[r];
@@ -142,20 +161,24 @@ __global__ __launch_bounds__(256) void ldlq_sub_kernel(float* __restrict__ wk, l
     __syncthreads();
     float e = 0.f;
 #pragma unroll
-    for (int k = 0; k < 16; k++) e = __fmaf_rn(s_err[r][k], uinv[(long)(s0 + k) * ldi + s0 + c], e);
+    for (int k = 0; k < 16; k++) e = __fmaf_rn(s_err[r][k], ui[k], e);
     __syncthreads();
     s_err[r][c] = e;
     __syncthreads();
-    // w[r][j] -= sum_k err[r][k] * U[s0+k][j] for j >= s1: thread (r, c) updates columns s1 + c, s1 + c + 16, ...
-    for (int j = s1 + c; j < 256; j += 16) {
-        float acc = 0.f;
+    // w[r][j] -= sum_k err[r][k] * U[s0+k][j] for j >= s1 (fma chain, k ascending); column s1 + c (m = 0) also
+    // gives the next sub-block's tile value
+    const float inv = 1.0f / dr;
 #pragma unroll
-        for (int k = 0; k < 16; k++) acc = __fmaf_rn(s_err[r][k], ublk[(long)(s0 + k) * ldu + j], acc);
-        wk[row * ldw + j] -= acc;
-    }
-    if (xnext && s1 < 256) {
-        const float inv = 1.0f / dr;
-        xnext[(long)blockIdx.x * 256 + tid] = wk[row * ldw + s1 + c] * inv;
+    for (int m = 0; m < 15; m++) {
+        if (m < nj) {
+            const int j = s1 + c + 16 * m;
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < 16; k++) acc = __fmaf_rn(s_err[r][k], s_u[k][j], acc);
+            const float nv = wj[m] - acc;
+            wk[row * ldw + j] = nv;
+            if (m == 0 && xnext) xnext[(long)blockIdx.x * 256 + tid] = nv * inv;
+        }
     }
 }
 
