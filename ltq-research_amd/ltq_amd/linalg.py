@@ -75,6 +75,10 @@ def cholesky_lower(A: torch.Tensor, leaf: int = LEAF, magma: bool = True) -> Tup
         r = _magma_cholesky(A)
         if r is not None:
             return r
+    if A.is_cuda:
+        # on the device the recursion has been measured correct with leaves of 1024 and 2048 rows (and 128) but
+        # failing (info != 0) with leaves of 256 and of 512 at K = 14336, cause not found; keep leaves >= 1024
+        leaf = max(leaf, 1024)
     if n <= leaf:
         L, info = cholesky_many(A.unsqueeze(0))
         return L[0], info[0]

@@ -79,3 +79,17 @@ def test_spd_solve_reads_only_the_lower_triangle():
     # indefinite: the LU fallback rebuilds the symmetric matrix from the lower triangle
     Ai = torch.tensor([[2.0, 99.0], [1.0, -1.0]])
     assert torch.allclose(linalg.spd_solve(Ai, torch.tensor([3.0, 0.0])), torch.tensor([1.0, 1.0]))
+
+
+@pytest.mark.gpu
+def test_recursive_cholesky_without_magma_gpu():
+    """The recursive factorization the device falls back to without MAGMA (leaves of at least 1024 rows through
+    the batched potrf, L21 by triangular solve, Schur complements by GEMM): info 0 and a float32 backward error."""
+    from ltq_amd import linalg
+    n = 5000
+    A = _spd(n, 11, "cuda")
+    print(f"recursive cholesky n={n}", flush=True)
+    L, info = linalg.cholesky_lower(A, leaf=256, magma=False)  # leaves are kept at >= 1024 rows on the device
+    assert int(info) == 0
+    Lc, Ad = torch.tril(L).double().cpu(), A.double().cpu()
+    assert (Lc @ Lc.T - Ad).abs().max() <= 1e-5 * Ad.abs().max()
