@@ -112,7 +112,8 @@ def cpu_model() -> str:
 
 
 def cpu_baseline_torch(inputs, budget_s, total_subblocks):
-    """BASELINE.md's CPU baseline: the reference's CPU path -- torch on the host, eager, every available core --
+    """The CPU baseline the benchmark plan specifies: the reference's CPU path -- torch on the host, eager, every
+    available core --
     over the first 256-column block of the same matrix with its LDLQ feedback (src/liqk_v2.py:948-970: torch
     matmuls), the Viterbi by oracle/torch_viterbi.py (the torch restatement of viterbi_ub with the kernel's D4 /
     tail-biting semantics). Sub-blocks run in order until budget_s is spent (at least one); the whole-matrix rate
@@ -376,7 +377,8 @@ class KernelTimer:
 
 C5_ROWS, C5_COLS = 262144, 2560  # K=4 D4 rings = TCQ375X; TCQ4X on request
 RING_SCALES = 3  # quantize_rings' scale candidates (src/ple_quant.py:53)
-# ring mode TCQ4X:rot (3 scales x 2 passes), 2.82e9 values in 33.18 s = 84.9 Mvalues/s (GPU unstated)
+# the reference's published ring-mode figure: TCQ4X:rot (3 scales x 2 passes), 2.82e9 values in 33.18 s = 84.9
+# Mvalues/s (GPU unstated)
 RING_PUBLISHED = {"TCQ4X": 84.9}
 
 
