@@ -113,8 +113,7 @@ def cpu_model() -> str:
 
 def cpu_baseline_torch(inputs, budget_s, total_subblocks):
     """The CPU baseline the benchmark plan specifies: the reference's CPU path -- torch on the host, eager, every
-    available core --
-    over the first 256-column block of the same matrix with its LDLQ feedback (src/liqk_v2.py:948-970: torch
+    available core -- over the first 256-column block of the same matrix with its LDLQ feedback (src/liqk_v2.py:948-970: torch
     matmuls), the Viterbi by oracle/torch_viterbi.py (the torch restatement of viterbi_ub with the kernel's D4 /
     tail-biting semantics). Sub-blocks run in order until budget_s is spent (at least one); the whole-matrix rate
     is extrapolated from them."""
