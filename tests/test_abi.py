@@ -94,3 +94,69 @@ def test_static_entry_refuses_oversized_calls_before_device_work():
     ints[3] = 250
     ints[16] = 256
     assert L.tcq_viterbi_static(*args, *ints, 2, None) == -1
+
+
+# tcq_viterbi's integer arguments, in order (the reference's ctypes binding, src/cuda/tcq_viterbi.cu:743-746)
+_VIT_INTS = ("mid_t", "tail", "N", "T", "S", "U", "G", "Gfull", "m", "sub", "U_hi", "mix", "m2", "m3", "m4", "nl",
+             "ld", "rot")
+_MAX = 4 * 128  # nl * U and nl * U_hi limit: 4 * MAX_U (tcq_viterbi.cu:17, 750)
+
+# (change to TCQ275X2's closing-pass arguments, whether the reference accepts it). Clauses of
+# src/cuda/tcq_viterbi.cu:748-751 (argument checks), 721-728 (G in {1, 2, 3, 4, 8}) and 763 (S in {256, 1024}).
+_VIT_RULES = [
+    ({}, True),
+    ({"G": 17}, False),                                   # G > MAX_G
+    ({"Gfull": 17, "gcand": True}, False),                # Gfull > MAX_G
+    ({"Gfull": 8}, False),                                # candidates (Gfull != G) without gcand
+    ({"Gfull": 8, "gcand": True}, True),
+    ({"U": 129}, False),                                  # U > MAX_U
+    ({"U_hi": 129}, False),                               # U_hi > MAX_U
+    ({"T": 248}, False),                                  # T % sub != 0
+    ({"sub": 6, "T": 36, "ld": 36, "pp": 0}, True),
+    ({"sub": 3, "T": 36, "ld": 36, "pp": 0}, False),      # odd sub
+    ({"sub": 8, "T": 264, "ld": 264}, False),             # T / sub > MAX_SUBS
+    ({"sub": 32, "T": 544, "ld": 544}, False),            # T > MAX_T
+    ({"sub": 32, "T": 512, "ld": 512}, True),
+    ({"sub": 34, "T": 68, "ld": 68, "pp": 0}, False),     # sub > 32
+    ({"nl": 32, "U": 1, "U_hi": 1, "sub": 32, "T": 256}, False),  # sub * G * nl * 2 > 4096 with pair parity
+    ({"nl": 32, "U": 1, "U_hi": 1, "sub": 32, "T": 256, "pp": 0, "G": 4}, True),  # 4096 without it
+    ({"S": 256, "nl": 4, "U": 8, "U_hi": 8}, False),      # pair parity needs S = 1024
+    ({"S": 256, "nl": 4, "U": 8, "U_hi": 8, "pp": 0}, True),
+    ({"S": 256, "pp": 0}, False),                         # S != 1024 needs nl = 4
+    ({"S": 512, "nl": 4, "U": 8, "U_hi": 8, "pp": 0}, False),  # S neither 1024 nor 256
+    ({"mix": 1}, False),                                  # pair parity with a mixed table
+    ({"sub": 18, "T": 36, "ld": 36}, False),              # D4 (pp >= 2) needs sub % 4 == 0
+    ({"sub": 18, "T": 36, "ld": 36, "pp": 1}, True),
+    ({"pp": 4}, False),                                   # pp > 3
+    ({"nl": 12}, False),                                  # nl not in {4, 8, 16, 32}
+    ({"ld": 255}, False),                                 # ld < T
+    ({"U": 65}, False),                                   # nl * U > 4 * MAX_U
+    ({"U": 64}, True),
+    ({"U_hi": 65}, False),                                # nl * U_hi > 4 * MAX_U
+    ({"G": 5, "Gfull": 5}, False),                        # no kernel for G = 5
+    ({"G": 8, "Gfull": 8}, True),
+]
+
+
+@pytest.mark.parametrize("change,accepted", _VIT_RULES, ids=[str(c) for c, _ in _VIT_RULES])
+def test_viterbi_argument_rules_match_the_reference_without_a_device(change, accepted):
+    """tcq_viterbi accepts and rejects the argument sets the reference does, before any device call: with N = 0 an
+    accepted set gets the zero-block launch's error (hipErrorInvalidConfiguration, 9, as CUDA's 9 for the
+    reference's <<<0, ...>>> launch) and a rejected one -1."""
+    from ltq_amd import _lib
+    so = ROOT / "ltq-research_amd" / "ltq_amd" / "libltq_hip.so"
+    if not so.exists():
+        pytest.skip("libltq_hip.so not built (run __graft_entry__.build())")
+    L = _lib.lib()
+    v = dict(mid_t=0, tail=1, N=0, T=256, S=1024, U=4, G=4, Gfull=4, m=359, sub=16, U_hi=4, mix=0, m2=241, m3=0, m4=0,
+             nl=8, ld=256, rot=128, pp=2, gcand=False)
+    v.update(change)
+    assert v["nl"] * v["U"] <= _MAX or not accepted
+    fake = 4096  # stand-in addresses: every call here returns before using them
+    ptrs = [fake] * 5 + [fake, None, None, None, None, None, fake if v["gcand"] else None, fake, None, None]
+    rc = L.tcq_viterbi(*ptrs, *[v[k] for k in _VIT_INTS], fake, v["pp"], None)
+    assert rc == (9 if accepted else -1)
+    # a negative tile count is rejected outright
+    if accepted:
+        v["N"] = -1
+        assert L.tcq_viterbi(*ptrs, *[v[k] for k in _VIT_INTS], fake, v["pp"], None) == -1
