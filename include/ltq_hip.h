@@ -63,7 +63,8 @@ int ltq_kernel_timing(void* start_event, void* stop_event, int launches);
  * dh[S, 16], bucket b = clamp(rint(x * inv_step + half_b), 0, nb - 1) picks a row of 64 candidates of lut[nb, 64];
  * the first candidate with the lowest sum_j dh (xs - lut[b_j][c])^2 gives out[S, 16] = lut[b_j][c]. Same
  * signature, argument meaning and results as src/cuda/tcq_viterbi.cu:806-811 (bound at src/tcq_proto.py:530-532),
- * with the rounding of nvcc's default contraction written out (fma for the bucket argument and the sums). */
+ * with the rounding of nvcc's default contraction written out (fma for the bucket argument and the sums).
+ * S = 0 returns hipErrorInvalidConfiguration (9), the reference's zero-block launch error; S < 0 or nb < 1: -1. */
 int lut_subs_quant(const float* xs, const float* dh, const float* lut, float* out, int S, float inv_step, float half_b,
                    int nb, void* stream);
 

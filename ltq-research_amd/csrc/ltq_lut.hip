@@ -73,7 +73,8 @@ extern "C" int lut_subs_quant(const float* xs, const float* dh, const float* lut
                               float half_b, int nb, void* stream)
 {
     if (S < 0 || nb < 1) return -1;
-    if (S == 0) return 0;
+    // no sub-blocks: the error of the zero-block launch the reference makes (its caller raises on it)
+    if (S == 0) return (int)hipErrorInvalidConfiguration;
     if (!xs || !dh || !lut || !out) return -1;
     long grid = ((long)S + kWaves - 1) / kWaves;
     if (grid > 1L << 20) grid = 1L << 20;

@@ -160,3 +160,18 @@ def test_viterbi_argument_rules_match_the_reference_without_a_device(change, acc
     if accepted:
         v["N"] = -1
         assert L.tcq_viterbi(*ptrs, *[v[k] for k in _VIT_INTS], fake, v["pp"], None) == -1
+
+
+def test_lut_subs_argument_rules_without_a_device():
+    """lut_subs_quant: no sub-blocks is the reference's zero-block launch, CUDA / HIP error 9, which its caller
+    raises on (src/cuda/tcq_viterbi.cu:806-811, src/tcq_proto.py:544-547); a negative count or an empty table -1.
+    All three return before any device call."""
+    from ltq_amd import _lib
+    so = ROOT / "ltq-research_amd" / "ltq_amd" / "libltq_hip.so"
+    if not so.exists():
+        pytest.skip("libltq_hip.so not built (run __graft_entry__.build())")
+    L = _lib.lib()
+    fake = 4096
+    assert L.lut_subs_quant(fake, fake, fake, fake, 0, 1.0, 8.0, 16, None) == 9
+    assert L.lut_subs_quant(fake, fake, fake, fake, -1, 1.0, 8.0, 16, None) == -1
+    assert L.lut_subs_quant(fake, fake, fake, fake, 4, 1.0, 8.0, 0, None) == -1

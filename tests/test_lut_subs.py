@@ -126,7 +126,8 @@ def test_gpu_lut_subs_argument_checks():
     x = torch.zeros((4, 16), device="cuda")
     t = torch.zeros((8, 64), device="cuda")
     L, st = _lib.lib(), _lib.stream_ptr()
-    assert L.lut_subs_quant(x.data_ptr(), x.data_ptr(), t.data_ptr(), x.data_ptr(), 0, 1.0, 0.0, 8, st) == 0
+    # no sub-blocks: the reference's zero-block launch error (9), on which its caller raises
+    assert L.lut_subs_quant(x.data_ptr(), x.data_ptr(), t.data_ptr(), x.data_ptr(), 0, 1.0, 0.0, 8, st) == 9
     assert L.lut_subs_quant(x.data_ptr(), x.data_ptr(), t.data_ptr(), x.data_ptr(), -1, 1.0, 0.0, 8, st) == -1
     assert L.lut_subs_quant(x.data_ptr(), x.data_ptr(), t.data_ptr(), x.data_ptr(), 4, 1.0, 0.0, 0, st) == -1
     torch.cuda.synchronize()
