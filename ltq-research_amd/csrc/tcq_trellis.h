@@ -142,8 +142,6 @@ struct Smem {
     int exch_floats;  // one exchange buffer (all gain slots)
     int dbl;          // exchange double-buffered
     int ring, nslot, slot_words;  // traceback ring (overlaps tables + exchange, dead after the forward pass)
-    int ncopy, nslot1;            // copier wavefronts of the streamlined walk; ring depth of the one-wave walk
-    int nres;                     // top ring slots beyond the forward pass's LDS: chunks written there directly
 };
 
 template <int NU, int RB, int MD, int NL>
@@ -180,30 +178,13 @@ LTQ_HD Smem smem_layout(int T, int G, int Gfull, int sub, int lds_max)
     const int cw = G * GE::Q * 64 * MM::NW;
     L.slot_words = ((cw + 255) / 256) * 256 + 256;  // + pad: the walker reads word w + 1 of any lane
     L.ring = L.tabs;
-    // The walk's copies of a chunk are split over ncopy wavefronts, each keeping nslot - 1 chunks of its share in
-    // flight (at most 63 outstanding: vmcnt). The copies come from global memory (~1 us away), so a deeper ring
-    // keeps more chunks in flight; a workgroup of 16 wavefronts has its CU to itself and may take up to 8 slots,
-    // smaller ones keep 4 so that several workgroups still share a CU. The walk of a single wavefront (nslot1)
-    // copies whole chunks itself.
+    // the copying wavefront keeps nslot - 1 chunks of copies in flight: at most 63 outstanding (vmcnt)
     const int nl = (cw / 4 + 63) / 64;
-    const int nwv = G * GE::Q;
-    const int side = nwv - 1 - (nwv - 1) / 4;  // waves off the walker's SIMD
-    L.ncopy = side < 3 ? (side > 1 ? side : 1) : 3;
-    const int nlc = (nl + L.ncopy - 1) / L.ncopy;
-    auto ring_fits = [&](int ns) {
-        return L.ring + ns * 4 * L.slot_words <= lds_max || L.ring + ns * 4 * L.slot_words <= fwd_end;
-    };
-    int ns = nwv >= 16 ? 8 : 4;
-    while (ns > 2 && (!ring_fits(ns) || (ns - 1) * nlc > 63)) ns--;
+    int ns = 4;
+    while (ns > 2 && ((L.ring + ns * 4 * L.slot_words > lds_max && L.ring + ns * 4 * L.slot_words > fwd_end) ||
+                      (ns - 1) * nl > 63))
+        ns--;
     L.nslot = ns;
-    int ns1 = ns;
-    while (ns1 > 2 && (ns1 - 1) * nl > 63) ns1--;
-    L.nslot1 = ns1;
-    // ring slots that start at or beyond the forward pass's LDS are free while it runs: the streamlined walk's
-    // chunks nchunk - 2 and nchunk - 3 are written there instead of to global memory, so the walk starts without
-    // waiting for copies
-    L.nres = 0;
-    while (L.nres < 2 && L.nres < ns - 1 && L.ring + (ns - 1 - L.nres) * 4 * L.slot_words >= fwd_end) L.nres++;
     const int ring_end = L.ring + ns * 4 * L.slot_words;
     L.total = fwd_end > ring_end ? fwd_end : ring_end;
     return L;
@@ -436,8 +417,7 @@ struct DecMap {
 // X provides: tid(), wave() (tid / 64, uniform), tile(), nthreads(), smem(), sync() (full barrier incl. global
 // memory), lds_sync() (barrier for LDS only), push_sign(acc, d), fmin(x, y), wave_min(v, i) (the wavefront's
 // (value, index) minimum, lowest index on ties, in lane 63), readlane(v, l) (lane l's value, l uniform), uni(v)
-// (a uniform value in a scalar register), pin(v) / pin_s(v) (v computed at this point, in a vector / scalar
-// register), sched_fence() (no instruction
+// (a uniform value in a scalar register), pin(v) (v computed at this point), sched_fence() (no instruction
 // moved across), load_coherent(p) (a global int written by this workgroup before a sync()), acquire()
 // (device-scope acquire: invalidates this CU's L1), load16(global src, LDS wave base) (asynchronous 16-byte
 // global -> LDS copy landing at base + 16 * lane), wait_loads(n) (at most n such copies of this wave still
@@ -696,11 +676,6 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
     uint32_t last_acc[NW];
 #pragma unroll
     for (int w = 0; w < NW; w++) last_acc[w] = 0;
-    // streamlined walk: chunk cc sits in ring slot (cc + roff) % nslot; roff puts the resident chunks
-    // nchunk - 2 .. nchunk - 1 - nres in the top slots (beyond the forward pass's LDS) and the last chunk in slot 0
-    const int nres = fast ? (SM.nres < nchunk - 1 ? SM.nres : nchunk - 1) : 0;
-    const int roff = ((SM.nslot + 1 - nchunk) % SM.nslot + SM.nslot) % SM.nslot;
-    auto rslot = [&](int cc) { return (uint32_t*)(sm + SM.ring) + ((cc + roff) % SM.nslot) * SM.slot_words; };
     // AL (whole chunks, sub-blocks a multiple of 16 steps): a sub-block can only end where the phase's end step is
     // a multiple of 16, so every other phase is compiled without the tile-end and merge tests (and without the
     // register copies a runtime merge branch costs in every phase)
@@ -861,10 +836,6 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
         if (fast && c == nchunk - 1) {
 #pragma unroll
             for (int w = 0; w < NW; w++) last_acc[w] = acc[w];
-        } else if (fast && c >= nchunk - 1 - nres) {  // resident chunk: straight into its ring slot
-            uint32_t* const slot = rslot(c);
-#pragma unroll
-            for (int w = 0; w < NW; w++) slot[((g * Q + q) * NW + w) * 64 + lane] = acc[w];
         } else if (Lb + 64L * nwc <= dm.cap_bp || Lb >= dm.cap_bp) {
             // the wave's words lie in one buffer: a scalar base, the lane offset and immediate word offsets
             uint32_t* const wb = Lb < dm.cap_bp ? dm.bp + Lb : dm.pb + (Lb - dm.cap_bp);
@@ -944,9 +915,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
     // block; that lane's decision bits give the phase's input state, the intermediate state and the parity
     // classes. Lanes of the walking wavefront fetch the possible next lookups one phase ahead; v_readlane
     // picks the true one.
-    // per phase: output state | slot << 10 | e << 13 | pa << 14 | (pa ^ pb) << 15 (pa, pb: the classes of steps
-    // ta, ta + 1; in D4 pa ^ pb is the class c* chosen by phase B, so a phase-B record takes its winner index as is)
-    uint16_t* s_rec = (uint16_t*)s_st;
+    uint16_t* s_rec = (uint16_t*)s_st;  // per phase: output state | slot << 10 | e << 13 | classes << 14
     // Streamlined walk (whole chunks, one block per lane, a second wavefront, a ring of at least 3 chunks,
     // sub-blocks of 16 or 32; every matrix-path tile): wavefront 0 walks, wavefront 1 copies the decision words of the chunks ahead
     // global -> LDS, one barrier per chunk hands them over, and every thread writes the outputs. Otherwise
@@ -965,26 +934,21 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
             uint32_t* ring = (uint32_t*)(sm + SM.ring);
             const int nslot = SM.nslot, slot_words = SM.slot_words;
             const int nloads = (G * Q * 16 * NW + 63) / 64;  // wave loads per chunk
-            // copier wavefronts: the first ncopy of waves 1, 2, 3, 5, 6, 7, ... (none on the walker's SIMD, as
-            // wavefront w runs on SIMD w % 4); copier c issues the wave loads i = c, c + ncopy, ... of every chunk
-            const int ncopy = SM.ncopy, cpy = wv - 1 - wv / 4;
-            const bool copier = (wv & 3) != 0 && cpy < ncopy;
-            const int my_loads = copier ? (nloads - cpy + ncopy - 1) / ncopy : 0;
             // copies of chunk cc: 16-byte units u = 64 i + lane; a chunk lies in bp or in pbits as a whole except
             // at most one, so the source is a uniform base plus the lane's offset (the last unit repeated past the
             // end: the copy then stays inside the chunk and lands in the slot's pad)
             auto issue = [&](int cc) {
                 const int units = G * Q * 16 * NW;
-                uint32_t* slot = rslot(cc);
+                uint32_t* slot = ring + (cc % nslot) * slot_words;
                 const long base = (long)cc * chunk_words;
                 if (base + chunk_words <= dm.cap_bp || base >= dm.cap_bp) {
                     const uint32_t* src = dm.at(base);
-                    for (int i = cpy; i < nloads; i += ncopy) {
+                    for (int i = 0; i < nloads; i++) {
                         const int u = i * 64 + lane;
                         X_.load16(src + 4L * (u < units ? u : units - 1), slot + i * 256);
                     }
                 } else {
-                    for (int i = cpy; i < nloads; i += ncopy) {
+                    for (int i = 0; i < nloads; i++) {
                         const int u = i * 64 + lane;
                         X_.load16(dm.at(base + 4L * (u < units ? u : units - 1)), slot + i * 256);
                     }
@@ -999,20 +963,13 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
             // first barrier the two the walk reads first (its chunk and, from its last phase on, the one below)
             // are in LDS
             {  // the last chunk's words from registers (the forward pass's LDS is free since the argmin barrier)
-                uint32_t* slot = rslot(nchunk - 1);
+                uint32_t* slot = ring + ((nchunk - 1) % nslot) * slot_words;
 #pragma unroll
                 for (int w = 0; w < NW; w++) slot[((g * Q + q) * NW + w) * 64 + lane] = last_acc[w];
             }
-            // chunks below the resident ones are copied; before a barrier, the chunk the walk reads next lands
-            const int top_copied = nchunk - 2 - nres;
-            // first copies: with a resident chunk below the last one the walk needs none of them before its first
-            // barrier, so they are issued inside the walk's first iteration instead of before this barrier
-            auto first_copies = [&]() {
-                for (int j = 1 + nres; j < nslot - 1 && nchunk - 1 - j >= 0; j++) issue(nchunk - 1 - j);
-            };
-            if (copier && nres == 0) {
-                first_copies();
-                X_.wait_loads(count(max_i(0, nchunk - nslot + 1), nchunk - 3) * my_loads);
+            if (wv == 1) {
+                for (int j = 1; j < nslot - 1 && nchunk - 1 - j >= 0; j++) issue(nchunk - 1 - j);
+                X_.wait_loads(count(max_i(0, nchunk - nslot + 1), nchunk - 3) * nloads);
             }
             X_.lds_sync();
             // per-lane hypothesis: L = lane & 3 (input-state bits h e), gp = lane >> 2 (gain slot at a boundary)
@@ -1024,7 +981,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
             uint32_t c0, c1, gv = 0;
             {  // exact words of the walk's first phase, in every lane
                 constexpr int P0 = MM::OFF(NPC - 1);
-                const uint32_t* slot = rslot(nchunk - 1);
+                const uint32_t* slot = ring + ((nchunk - 1) % nslot) * slot_words;
                 const int wi = ((gs * Q + ((st >> 8) & (Q - 1))) * NW + (P0 >> 5)) * 64 + ((st >> 2) & 63);
                 c0 = slot[wi];
                 c1 = slot[wi + 64];
@@ -1034,56 +991,24 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
             // word offset of this lane's hypothesis (wave and lane bits of start(hypL, 0, 0), disjoint from those of
             // start(0, q, l)) in a ring slot, for the phases that cannot start a sub-block
             const int lane_off = wL * NW * 64 + lL;
-            // Register walk (every sub-block boundary at a chunk start): the walked chunk's words of the path's gain
-            // slot sit in this wave's registers. A phase's word is indexed by qi = (wave << 6) | lane of its output
-            // state, and the state below a phase is start(L, qq, ll), so qi of the phase below is
-            // (L << (4 + QB)) | (qq << 4) | (ll >> 2): its low 4 + QB bits are known before the decode. Lane
-            // (a << 4) | lo holds in R[hi][w] word w of qi = (a << (4 + QB)) | (hi << 4) | lo: the next phase's row hi
-            // = qq is chosen while this phase decodes, and v_readlane at lane (L << 4) | lo fetches the word once L is
-            // known -- no LDS round trip between two phases of a chunk.
-            uint32_t R[Q][NW];
-            const int r_a = lane >> 4, r_lo = lane & 15;
-            auto load_regs = [&](const uint32_t* slot, int gsl) {
-#pragma unroll
-                for (int hi = 0; hi < Q; hi++) {
-                    const int qi = (r_a << (4 + QB)) | (hi << 4) | r_lo;
-                    const uint32_t* src = slot + (gsl * Q + (qi >> 6)) * NW * 64 + (qi & 63);
-#pragma unroll
-                    for (int w = 0; w < NW; w++) R[hi][w] = src[w * 64];
-                }
-            };
-            // row hi is uniform: the register array is indexed through the GPR index mode (s_set_gpr_idx_on /
-            // v_mov / off), four scalar + vector instructions a word instead of a three-deep v_cndmask tree
-            auto pick_row = [&](int hi, int w) -> uint32_t { return R[X_.uni(hi)][w]; };
-            const bool rw = (sub % CK) == 0;
             // The walk over chunks kmax .. : MIDW (first tail-biting pass) stops at the phase holding mid_t and writes
             // no records; the full walk keeps every phase's 16-bit record in scalar registers and stores a chunk's
             // records, two a word, at the end of the chunk. A sub-block can only start at a phase with 2 pi a
             // multiple of 16 (sub is 16 or 32), so every other phase carries no boundary test, no merge-choice fetch
             // and a scalar word address.
-            auto walk = [&](auto midw, auto rwc) {
+            auto walk = [&](auto midw) {
                 constexpr bool MIDW = decltype(midw)::value;
-                constexpr bool RW = decltype(rwc)::value;
                 bool stop = false;
-                if constexpr (RW) {
-                    if (wv == 0) load_regs(rslot(nchunk - 1), gs);
-                }
-                // ring slot of chunk cc, stepped down with cc (no division in the loop)
-                int si = (nchunk - 1 + roff) % nslot;
-                uint32_t* const ring0 = (uint32_t*)(sm + SM.ring);
                 for (int k = 0; k < kmax; k++) {
                     const int cc = nchunk - 1 - k;
-                    const int si_next = si == 0 ? nslot - 1 : si - 1;  // chunk cc - 1
-                    if (copier) {  // chunk cc - nslot + 1 into the slot chunk cc + 1 left; chunk cc - 2 lands first
-                        if (k == 0 && nres > 0) first_copies();
-                        if (cc - nslot + 1 >= 0 && cc - nslot + 1 <= top_copied) issue(cc - nslot + 1);
-                        X_.wait_loads(count(max_i(0, cc - nslot + 1), min_i(cc - 3, top_copied)) * my_loads);
+                    if (wv == 1) {  // chunk cc - nslot + 1 into the slot chunk cc + 1 left; chunk cc - 2 lands first
+                        if (cc - nslot + 1 >= 0) issue(cc - nslot + 1);
+                        X_.wait_loads(count(max_i(0, cc - nslot + 1), cc - 3) * nloads);
                     }
                     if (wv == 0) {
-                        const uint32_t* slot = ring0 + si * slot_words;
-                        const uint32_t* slot_next = ring0 + si_next * slot_words;
-                        // the chunk's records, two a word (phase 2 w + 1 in the high half), built phase by phase
-                        uint32_t recw[NPC / 2];
+                        const uint32_t* slot = ring + (cc % nslot) * slot_words;
+                        const uint32_t* slot_next = ring + ((cc + nslot - 1) % nslot) * slot_words;  // chunk cc - 1
+                        uint32_t recs[NPC];
                         static_for<0, NPC>([&](auto Kc) {
                             constexpr int pi = NPC - 1 - decltype(Kc)::value;
                             constexpr int PT = MM::PT(pi);
@@ -1108,12 +1033,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                             // after this phase's words are read (so the wait for those does not cover them) and
                             // before the decode, which they overlap; the fences keep the compiler from moving them.
                             uint32_t n0 = c0, n1 = c1;
-                            if (RW && pi > 0) {  // the phase below, in this chunk: its row of the register copy
-                                constexpr int PNw = MM::OFF(pi - 1) >> 5;
-                                const int hi = (st >> 8) & (Q - 1);
-                                n0 = pick_row(hi, PNw);
-                                if constexpr (PNw + 1 < NW) n1 = pick_row(hi, PNw + 1);
-                            } else if (pi > 0 || cc > 0) {
+                            if (pi > 0 || cc > 0) {
                                 constexpr int PN = pi > 0 ? pi - 1 : NPC - 1;
                                 constexpr int PNw = MM::OFF(PN) >> 5;
                                 const int su = GE::start(0, qq, ll);
@@ -1182,26 +1102,15 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                                     return;
                                 }
                             } else {
-                                const uint32_t rec = (uint32_t)(st | (gs << 10) | (e << 13) | (pa << 14) | ((pa ^ pb) << 15));
-                                if constexpr (pi & 1) {
-                                    recw[pi / 2] = rec << 16;
-                                } else {
-                                    recw[pi / 2] |= rec;
-                                    X_.pin_s(recw[pi / 2]);  // built now: no per-phase fields stay live to the chunk end
-                                }
+                                recs[pi] = (uint32_t)(st | (gs << 10) | (e << 13) | (pa << 14) | (pb << 15));
                             }
                             const int Ln = X_.uni(2 * h + e);
                             st = X_.uni(GE::start(Ln, qq, ll));  // state at step ta - 1
-                            sel = (RW && pi > 0) ? (Ln << 4) | ((st >> 2) & 15) : Ln;
+                            sel = Ln;
                             cstar = X_.uni(cstar);
                             if (bnd) {  // sub-block start: the path came from the slot the merge chose
                                 gs = (int)X_.readlane(gv, Ln);
                                 sel = Ln + 4 * gs;
-                            }
-                            if constexpr (RW) {
-                                // chunk cc - 1, the path's slot (for cc = 0 an unused in-bounds copy of chunk 0's
-                                // slot: an unconditional load lands straight in R, waited for at its first use)
-                                if (pi == 0) load_regs(cc > 0 ? slot_next : slot, gs);
                             }
                         });
                         if constexpr (!MIDW) {
@@ -1209,23 +1118,19 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                                 uint32_t* dst = (uint32_t*)s_rec + cc * (NPC / 2);
                                 static_for<0, NPC / 2>([&](auto Wc) {
                                     constexpr int w = decltype(Wc)::value;
-                                    dst[w] = recw[w];
+                                    dst[w] = recs[2 * w] | (recs[2 * w + 1] << 16);
                                 });
                             }
                         }
                     }
                     X_.lds_sync();  // the records of chunk cc are written; chunk cc - 2 is in LDS; slot of cc + 1 free
-                    si = si_next;
                 }
             };
-            if (a.mid_st) {
-                if (rw) walk(std::true_type{}, std::true_type{});
-                else walk(std::true_type{}, std::false_type{});
-            } else {
-                if (rw) walk(std::false_type{}, std::true_type{});
-                else walk(std::false_type{}, std::false_type{});
-            }
-            if (copier) X_.wait_loads(0);  // no copy may still land in this workgroup's LDS after it ends
+            if (a.mid_st)
+                walk(std::true_type{});
+            else
+                walk(std::false_type{});
+            if (wv == 1) X_.wait_loads(0);  // no copy may still land in this workgroup's LDS after it ends
             if (wv == 0 && lane == 0) {
                 if (a.mid_st) a.mid_st[n] = mid_val;
                 a.best[n] = bi_all;
@@ -1236,7 +1141,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
     }
     if (!fast) {
         uint32_t* ring = (uint32_t*)(sm + SM.ring);
-        const int nslot = SM.nslot1, slot_words = SM.slot_words;
+        const int nslot = SM.nslot, slot_words = SM.slot_words;
         const uint32_t* dummy = dm.bp;
         auto chunk_nwc = [&](int cc) {
             const int rp = (cc + 1) * NPC <= nph ? NPC : nph - cc * NPC;
@@ -1346,7 +1251,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
                 }
                 const int ph = ta >> 1;
                 // the phase's output state, slot, intermediate bit and classes (the step-ta state follows from them)
-                s_rec[ph] = (uint16_t)(st | (gs << 10) | (e << 13) | (pa << 14) | ((pa ^ pb) << 15));
+                s_rec[ph] = (uint16_t)(st | (gs << 10) | (e << 13) | (pa << 14) | (pb << 15));
                 if (ph == mid_ph) {  // first tail-biting pass: only the state before mid_t is needed
                     if (lane == 0) a.mid_st[n] = (a.mid_t - 1) & 1 ? st : GE::mid(bb, 2 * ca + e, qq, ll);
                     done = true;
@@ -1384,7 +1289,7 @@ LTQ_DEV void tcq_tile(const TcqArgs& a, X& X_, int lds_max, int init_val = -1)
         const int stt = (t & 1) ? so
                                 : GE::mid(so >> (8 + QB), 2 * ((so >> 1) & 1) + ((rr >> 13) & 1), (so >> 8) & (Q - 1),
                                           (so >> 2) & 63);
-        const int par = ((rr >> 14) ^ ((t & 1) ? rr >> 15 : 0)) & 1;  // pa, or pb = pa ^ (pa ^ pb)
+        const int par = (rr >> ((t & 1) ? 15 : 14)) & 1;
         const int lb = mk.label(stt);
         const bool hi = mix > 0 && ((t / mix) & 1);
         const int Ut = hi ? U_hi : U;

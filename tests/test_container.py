@@ -4,7 +4,8 @@ CPU: the file layout (magic, version, reserve, 4096-aligned data, 64-byte aligne
 header), every tensor dtype and the header's format description read back exactly.
 GPU: the HIP slice decoder reproduces the reference's own decoded values for 12 formats (tests/golden/
 packing.npz), and quantize -> LtqWriter.add_matrix (decode-verified) -> LtqFile.decode_matrix gives the
-quantizer's reconstruction bit for bit, for a single-format matrix and for row slices of two formats.
+quantizer's reconstruction bit for bit, for a single-format matrix and for row slices of two formats, and at the
+benchmark's full C3 size.
 """
 import struct
 
@@ -99,4 +100,39 @@ def test_gpu_quantize_write_read_decode(tmp_path, specs):
     assert nbytes > 0
     Wd = LtqFile(p).decode_matrix("layer.w", device="cuda")
     torch.cuda.synchronize()
+    assert torch.equal(Wd.view(torch.int32), W_hat.float().contiguous().view(torch.int32))
+
+
+@pytest.mark.gpu
+def test_gpu_full_c3_write_read_decode(tmp_path):
+    """The benchmark's C3 matrix (4096 x 14336 bf16 Student-t with outlier columns, H from 2048 activation rows,
+    TCQ275X2) through quantize -> .ltq -> decode at full size (256 row groups x 56 column blocks): the file holds
+    M K 2.75 / 8 bytes of codes plus the gain indices and decodes to the quantizer's reconstruction bit for bit."""
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+    import bench
+    from ltq_amd import liqk
+    from ltq_amd.formats import make_format
+    from ltq_amd.ltq_file import LtqFile, LtqWriter, format_json
+    print("full C3 quantize -> .ltq -> decode", flush=True)
+    W, H, _ = bench.prepare(torch.device("cuda"))
+    liqk.PACK = {}
+    try:
+        q, W_hat, rel = liqk.quantize_matrix_liqk_v2(W, H, "TCQ275X2", damp=0.02)
+        pm = liqk.PACK["matrix"]
+    finally:
+        liqk.PACK = None
+    del H
+    f = make_format("TCQ275X2")
+    p = tmp_path / "c3.ltq"
+    w = LtqWriter(p, [f], reserve=RESERVE)
+    nbytes = w.add_matrix("down_proj", pm, verify=True)
+    w.finalize({"quantization": {"formats": [format_json(f)]}})
+    M, K = W.shape
+    print(f"full C3: {nbytes} bytes, relative proxy loss {rel:.6f}", flush=True)
+    assert nbytes >= M * K * 11 // 32
+    Wd = LtqFile(p).decode_matrix("down_proj", device="cuda")
+    torch.cuda.synchronize()
+    assert Wd.shape == (M, K)
     assert torch.equal(Wd.view(torch.int32), W_hat.float().contiguous().view(torch.int32))
