@@ -67,6 +67,9 @@ SINGLE = [  # kwargs of one kernel call (reference ABI semantics)
     dict(nu=10, nl_ext=(), G=2, T=256, U=2, pp=1),
     dict(nu=10, nl_ext=(), G=4, T=256, U=4, pp=1),
     dict(nu=10, nl_ext=(241,), G=2, T=256, U=2, pp=3),
+    # the reference's limits: the longest tile (MAX_T = 512) in D4, and the largest metric table (sub G nl = 4096)
+    dict(nu=10, nl_ext=(241,), G=4, T=512, U=4, pp=2, sub=32),
+    dict(nu=10, nl_ext=(211, 397, 58), G=4, T=64, U=4, pp=0, sub=32),
 ]
 
 

@@ -47,6 +47,9 @@ CASES = [
     dict(pp=1, ext=(), G=2, T=64, U=2),
     dict(pp=1, ext=(), G=4, T=64, U=4),
     dict(pp=3, ext=(241,), G=2, T=32, U=2),
+    # the reference's limits: the longest tile (MAX_T = 512) in D4, and the largest metric table (sub G nl = 4096)
+    dict(pp=2, ext=(241,), G=4, T=512, sub=32),
+    dict(pp=0, ext=(211, 397, 58), G=4, T=64, sub=32),
 ]
 
 
