@@ -4,6 +4,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -175,3 +176,67 @@ def test_lut_subs_argument_rules_without_a_device():
     assert L.lut_subs_quant(fake, fake, fake, fake, 0, 1.0, 8.0, 16, None) == 9
     assert L.lut_subs_quant(fake, fake, fake, fake, -1, 1.0, 8.0, 16, None) == -1
     assert L.lut_subs_quant(fake, fake, fake, fake, 4, 1.0, 8.0, 0, None) == -1
+
+
+@pytest.mark.parametrize("K,frac,h,sub", [(2, 1, 0, 32), (3, 2, 2, 16), (3, 1, 3, 32), (4, 0, 4, 64), (5, 2, 8, 16),
+                                          (8, 1, 5, 256), (4, 1, 3, 4)])
+def test_slice_bytes_equal_the_oracle_layout_without_a_device(K, frac, h, sub):
+    """ltq_slice_bytes (what the packer and the decoder size their buffers by) equals the length of the oracle's
+    packed slice (src/ltq_file.py:79-102: four regions, each on a 64-byte boundary) for ragged row-group and
+    column-block counts; sizes off the 16 x 16 tile grid, negative sizes and unknown formats are -1."""
+    from ltq_amd import _lib
+    from oracle import pack
+    so = ROOT / "ltq-research_amd" / "ltq_amd" / "libltq_hip.so"
+    if not so.exists():
+        pytest.skip("libltq_hip.so not built (run __graft_entry__.build())")
+    L = _lib.lib()
+    rng = np.random.default_rng(K * 100 + sub)
+    for R, Kc in ((16, 16), (48, 16 * 37), (32, 256)):
+        idx = rng.integers(0, 1 << 15, (R, Kc)).astype(np.int16)
+        gi = rng.integers(0, 256, (R, Kc)).astype(np.uint8)
+        assert L.ltq_slice_bytes(R, Kc, K, frac, h, sub) == len(pack.pack_slice(idx, gi, K, frac, h, sub))
+    assert L.ltq_slice_bytes(0, 0, K, frac, h, sub) == 0
+    assert L.ltq_slice_bytes(24, 16, K, frac, h, sub) == -1
+    assert L.ltq_slice_bytes(16, 40, K, frac, h, sub) == -1
+    assert L.ltq_slice_bytes(-16, 16, K, frac, h, sub) == -1
+    assert L.ltq_slice_bytes(16, 16, K, frac, h, 3) == -1
+
+
+def test_hbm_entry_points_argument_rules_without_a_device():
+    """The rotation, row-scale and packing entry points return 0 for empty inputs and -1 for shapes, strides,
+    modes or pointers they cannot serve, all before any device call."""
+    from ltq_amd import _lib
+    so = ROOT / "ltq-research_amd" / "ltq_amd" / "libltq_hip.so"
+    if not so.exists():
+        pytest.skip("libltq_hip.so not built (run __graft_entry__.build())")
+    L = _lib.lib()
+    a = 4096  # stand-in address, 16-byte aligned; every call here returns before using it
+    # FWHT along rows: (x, dtype, y, rows, cols, ldx, ldy, s, smode)
+    assert L.ltq_fwht256_rows(a, 0, a, 0, 512, 512, 512, None, 0, None) == 0
+    assert L.ltq_fwht256_rows(a, 0, a, 4, 0, 0, 0, None, 0, None) == 0
+    assert L.ltq_fwht256_rows(a, 0, a, 4, 300, 300, 300, None, 0, None) == -1    # cols not a multiple of 256
+    assert L.ltq_fwht256_rows(a, 0, a, 4, 512, 256, 512, None, 0, None) == -1    # ldx < cols
+    assert L.ltq_fwht256_rows(a, 0, a, 4, 512, 514, 512, None, 0, None) == -1    # ldx not a multiple of 4
+    assert L.ltq_fwht256_rows(a, 3, a, 4, 512, 512, 512, None, 0, None) == -1    # element type
+    assert L.ltq_fwht256_rows(a, 0, a, 4, 512, 512, 512, None, 1, None) == -1    # scale mode without a scale
+    assert L.ltq_fwht256_rows(a + 4, 0, a, 4, 512, 512, 512, None, 0, None) == -1  # fp32 rows need 16-byte alignment
+    # FWHT along columns: (x, y, rows, cols, ldx, ldy, s, smode)
+    assert L.ltq_fwht256_cols(a, a, 0, 64, 64, 64, None, 0, None) == 0
+    assert L.ltq_fwht256_cols(a, a, 300, 64, 64, 64, None, 0, None) == -1       # rows not a multiple of 256
+    assert L.ltq_fwht256_cols(a, a, 256, 64, 32, 64, None, 0, None) == -1       # ldx < cols
+    assert L.ltq_fwht256_cols(a, a, 256, 64, 64, 64, None, 3, None) == -1       # scale mode
+    # row scale: (w, M, K, ldw, scale, e_step, e_bits, exp2_tab, d_row, e, lde, d, ldd)
+    assert L.ltq_row_scale(a, 0, 512, 512, 1.1, 0.25, 5, a, a, a, 2, a, 2, None) == 0
+    assert L.ltq_row_scale(a, 16, 300, 300, 1.1, 0.25, 5, a, a, a, 2, a, 2, None) == -1  # K not a multiple of 256
+    assert L.ltq_row_scale(a, 16, 512, 512, 1.1, 0.25, 9, a, a, a, 2, a, 2, None) == -1  # e_bits
+    assert L.ltq_row_scale(a, 16, 512, 512, 0.0, 0.25, 5, a, a, a, 2, a, 2, None) == -1  # scale
+    assert L.ltq_row_scale(a, 16, 512, 512, 1.1, 0.25, 5, a, a, a, 1, a, 2, None) == -1  # lde < blocks
+    # packing and decoding: an output smaller than the slice, or strides below K
+    need = L.ltq_slice_bytes(16, 256, 3, 2, 2, 16)
+    assert need > 0
+    assert L.ltq_pack_slice(a, 256, a, 256, 0, 0, 3, 2, 2, 16, a, 0, None) == 0
+    assert L.ltq_pack_slice(a, 256, a, 256, 16, 256, 3, 2, 2, 16, a, need - 1, None) == -1
+    assert L.ltq_pack_slice(a, 255, a, 256, 16, 256, 3, 2, 2, 16, a, need, None) == -1
+    assert L.ltq_unpack_slice(a, need - 1, 16, 256, 3, 2, 2, 16, 359, 241, 0, 0, 2, a, a, a, 256, None) == -1
+    assert L.ltq_unpack_slice(a, need, 16, 256, 3, 2, 2, 16, 359, 241, 0, 0, 5, a, a, a, 256, None) == -1  # masks
+    assert L.ltq_unpack_slice(a, need, 16, 256, 3, 2, 2, 16, 359, 241, 0, 0, 2, a, a, a, 255, None) == -1  # ld_out
