@@ -1354,7 +1354,9 @@ inline int tcq_check(const TcqArgs& a)
         nl * U_hi > 4 * kMaxU)
         return -1;
     if ((S != 1024 && S != 256) || (G != 1 && G != 2 && G != 3 && G != 4 && G != 8)) return -1;
-    if (T <= 0 || !a.bp || (pp && !a.pbits && a.tile_words <= 0) || !a.best || !a.rec) return -1;
+    // buffers are checked only when there are tiles: with none, torch hands over null pointers and the call must
+    // reach the zero-tile return code, as the reference's unchecked zero-block launch does
+    if (T <= 0 || (a.N > 0 && (!a.bp || (pp && !a.pbits && a.tile_words <= 0) || !a.best || !a.rec))) return -1;
     return 0;
 }
 

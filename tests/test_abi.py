@@ -157,6 +157,11 @@ def test_viterbi_argument_rules_match_the_reference_without_a_device(change, acc
     ptrs = [fake] * 5 + [fake, None, None, None, None, None, fake if v["gcand"] else None, fake, None, None]
     rc = L.tcq_viterbi(*ptrs, *[v[k] for k in _VIT_INTS], fake, v["pp"], None)
     assert rc == (9 if accepted else -1)
+    # with no tiles, empty torch buffers arrive as null pointers: still the zero-block launch's error, not -1
+    if accepted:
+        nulls = [fake, fake, fake, fake, None, None, None, None, None, None, None, fake if v["gcand"] else None, None,
+                 None, None]
+        assert L.tcq_viterbi(*nulls, *[v[k] for k in _VIT_INTS], None, v["pp"], None) == 9
     # a negative tile count is rejected outright
     if accepted:
         v["N"] = -1

@@ -255,3 +255,20 @@ def test_gpu_timing_hook_keeps_results_and_times_the_launches(tp):
     ms = [e0.elapsed_time(e1) for e0, e1 in recs[0]["ev"]]
     print(f"pass 1 / pass 2 over 64 tiles: {ms[0] * 1e3:.1f} / {ms[1] * 1e3:.1f} us", flush=True)
     assert all(0.0 < t < 50.0 for t in ms) and ms[0] < ms[1]
+
+
+@pytest.mark.gpu
+def test_gpu_empty_inputs_behave_like_the_reference(tp):
+    """Empty inputs: the FWHT of no rows is an empty tensor, as torch's transform gives (src/iqk_format.py:153-170);
+    a Viterbi call over no tiles and a LUT call over no sub-blocks raise, as the reference's callers raise on the
+    error 9 of its zero-block launches (src/tcq_proto.py:544-547 and the tcq_viterbi return-code check)."""
+    from ltq_amd.rotation import fwht_cols, fwht_rows
+    print("empty inputs", flush=True)
+    assert fwht_rows(torch.zeros((0, 512), device=DEV)).shape == (0, 512)
+    assert fwht_cols(torch.zeros((0, 64), device=DEV)).shape == (0, 64)
+    with pytest.raises(RuntimeError, match="9"):
+        tp.viterbi_ub_cuda(torch.zeros((0, 32), device=DEV), torch.zeros(16, device=DEV), 3, 10, 359)
+    with pytest.raises(RuntimeError, match="9"):
+        tp.lut_subs_quant_cuda(torch.zeros((0, 16), device=DEV), torch.zeros((0, 16), device=DEV),
+                               torch.zeros((8, 64), device=DEV), 1.0, 4.0)
+    torch.cuda.synchronize()
